@@ -1,0 +1,24 @@
+"""MI355X-native chunkwise gated delta-rule attention (KDA, Gated DeltaNet, GLA, DeltaNet).
+
+The export surface mirrors the reference's op package for this family (src/ops/__init__.py:1-6): a
+`chunk_*` (prefill) and a `recurrent_*` (decode) function per variant, backed by the hand-written gfx950 HIP
+kernels of libgdr.so.  `RecurrentCache` mirrors the decode-state owner of src/cache.py:48-86.
+"""
+
+from .cache import RecurrentCache
+from .deltanet import chunk_deltanet, recurrent_deltanet
+from .gated_deltanet import chunk_gated_deltanet, recurrent_gated_deltanet
+from .gated_linear_attention import chunk_gated_linear_attention, recurrent_gated_linear_attention
+from .kimi_delta_attention import chunk_kimi_delta_attention, recurrent_kimi_delta_attention
+
+__all__ = [
+    "RecurrentCache",
+    "chunk_deltanet",
+    "chunk_gated_deltanet",
+    "chunk_gated_linear_attention",
+    "chunk_kimi_delta_attention",
+    "recurrent_deltanet",
+    "recurrent_gated_deltanet",
+    "recurrent_gated_linear_attention",
+    "recurrent_kimi_delta_attention",
+]

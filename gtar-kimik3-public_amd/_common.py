@@ -1,0 +1,109 @@
+"""Host-side glue shared by the four op modules: argument resolution, validation and the libgdr launch.
+
+Mirrors the reference's per-op host code (src/ops/kimi_delta_attention.py:625-692 and the identical helpers in
+gated_deltanet.py:472-520, gated_linear_attention.py:437-483, deltanet.py:399-445):
+  * scale = `scale or head_dim ** -0.5` (so 0.0 also selects the default, as in the reference),
+  * the chunk path casts q, k, v to the autocast dtype when autocast is enabled (utils.py:84-88),
+  * a missing initial state is a zero fp32 state, a given one is used as `initial_state.float().contiguous()`,
+  * the final state is always a fresh fp32 tensor and inputs are never modified,
+  * the output has the value's dtype; `(out, final_state)` is returned only when `output_final_state`.
+Differences, all deliberate: CPU tensors raise (the reference's CPU token loop is this repository's test oracle,
+not a product path); requesting gradients raises (the forward-only kernels have no backward yet); packed
+variable-length input is accepted through `cu_seqlens` (the reference has none).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_VARIANT_NAMES = {_lib.KDA: "kimi delta attention", _lib.GDN: "gated deltanet", _lib.GLA: "gated linear attention",
+                  _lib.DELTANET: "deltanet"}
+
+
+def _autocast(*tensors):
+    if torch.is_autocast_enabled("cuda"):
+        dtype = torch.get_autocast_dtype("cuda")
+        return [x.to(dtype) for x in tensors]
+    return list(tensors)
+
+
+def _check_no_grad(*tensors):
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise NotImplementedError(
+            "the gfx950 gated delta-rule kernels are forward-only; run under torch.no_grad() or detach the inputs"
+        )
+
+
+def _aligned(x: torch.Tensor) -> bool:
+    es = x.element_size()
+    return x.data_ptr() % 16 == 0 and all((s * es) % 16 == 0 for s in x.stride()[:3])
+
+
+def _as_row_aligned(x: torch.Tensor) -> torch.Tensor:
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    return x if _aligned(x) else x.contiguous()
+
+
+def run(variant: int, chunk: bool, query, key, value, gate, beta, scale, initial_state, output_final_state,
+        cu_seqlens=None):
+    name = _VARIANT_NAMES[variant]
+    _check_no_grad(query, key, value, gate, beta, initial_state)
+    tensors = [t for t in (query, key, value, gate, beta, initial_state, cu_seqlens) if t is not None]
+    if not all(t.is_cuda for t in tensors):
+        raise ValueError(f"{name}: all tensors must be on the GPU (this implementation has no CPU path)")
+    device = query.device
+    if any(t.device != device for t in tensors):
+        raise ValueError(f"{name}: all tensors must be on one device")
+    if query.dim() != 4 or key.shape != query.shape or value.dim() != 4 or value.shape[:3] != query.shape[:3]:
+        raise ValueError(f"{name}: expected q, k [B,H,T,K] and v [B,H,T,V], got {tuple(query.shape)}, "
+                         f"{tuple(key.shape)}, {tuple(value.shape)}")
+    batch, heads, seq_len, key_dim = query.shape
+    value_dim = value.shape[-1]
+
+    scale = scale or key_dim ** -0.5
+    if chunk:
+        query, key, value = _autocast(query, key, value)
+    out_dtype = value.dtype
+
+    if gate is not None:
+        expect = (batch, heads, seq_len) if variant == _lib.GDN else (batch, heads, seq_len, key_dim)
+        if tuple(gate.shape) != expect:
+            raise ValueError(f"{name}: gate must have shape {expect}, got {tuple(gate.shape)}")
+        gate = gate.float()
+    if beta is not None:
+        if tuple(beta.shape) != (batch, heads, seq_len):
+            raise ValueError(f"{name}: beta must have shape {(batch, heads, seq_len)}, got {tuple(beta.shape)}")
+        beta = beta.float()
+
+    n_states = batch
+    if cu_seqlens is not None:
+        if not chunk:
+            raise ValueError(f"{name}: cu_seqlens is only supported by the chunk op")
+        if batch != 1:
+            raise ValueError(f"{name}: cu_seqlens requires batch size 1 (packed sequences), got {batch}")
+        cu_seqlens = cu_seqlens.to(torch.int32).contiguous()
+        n_states = cu_seqlens.numel() - 1
+        if n_states < 1:
+            raise ValueError(f"{name}: cu_seqlens needs at least two offsets")
+
+    state_shape = (n_states, heads, key_dim, value_dim)
+    if initial_state is not None:
+        if tuple(initial_state.shape) != state_shape:
+            raise ValueError(f"{name}: initial_state must have shape {state_shape}, got {tuple(initial_state.shape)}")
+        initial_state = initial_state.float().contiguous()
+
+    if chunk:
+        # The chunk kernel runs its matrix products in bf16 on MFMA; it reads bf16 q, k, v with 16-byte rows.
+        query, key, value = (x.to(torch.bfloat16) for x in (query, key, value))
+        query, key, value = (_as_row_aligned(x) for x in (query, key, value))
+        if gate is not None and variant != _lib.GDN:
+            gate = _as_row_aligned(gate)
+
+    out = torch.empty(batch, heads, seq_len, value_dim, device=device, dtype=out_dtype)
+    final_state = torch.empty(state_shape, device=device, dtype=torch.float32) if output_final_state else None
+    args = _lib.make_args(variant, query, key, value, gate, beta, out, scale, initial_state, final_state, cu_seqlens)
+    _lib.launch("gdr_chunk_fwd" if chunk else "gdr_recurrent_fwd", args, device)
+    return (out, final_state) if output_final_state else out

@@ -1,0 +1,139 @@
+"""ctypes binding of libgdr.so, the hand-written gfx950 HIP library behind every op in this package.
+
+The library exposes the C ABI declared in include/gdr.h.  This module mirrors its two structs, loads the shared
+object that sits next to this file (built in place by csrc/Makefile), converts torch tensors into strided views
+(device pointer + dtype code + b/h/t element strides) and launches on torch's current HIP stream.
+
+There is deliberately no fallback: if the library is missing or the tensors are not on the GPU, the call
+raises.  The CPU restatement of the reference algorithm lives under oracle/ and is test infrastructure only.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY_PATH = os.path.join(_HERE, "libgdr.so")
+ABI_VERSION = 1
+
+KDA, GDN, GLA, DELTANET = 0, 1, 2, 3
+F32, BF16, F16 = 0, 1, 2
+_DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+
+class GdrTensor(ctypes.Structure):
+    _fields_ = [
+        ("ptr", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("stride_b", ctypes.c_int64),
+        ("stride_h", ctypes.c_int64),
+        ("stride_t", ctypes.c_int64),
+    ]
+
+
+class GdrArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("variant", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("seq_len", ctypes.c_int32),
+        ("key_dim", ctypes.c_int32),
+        ("value_dim", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("q", GdrTensor),
+        ("k", GdrTensor),
+        ("v", GdrTensor),
+        ("gate", GdrTensor),
+        ("beta", GdrTensor),
+        ("out", GdrTensor),
+        ("h0", ctypes.c_void_p),
+        ("ht", ctypes.c_void_p),
+        ("cu_seqlens", ctypes.c_void_p),
+        ("n_seqs", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+# Every symbol include/gdr.h declares, with its ctypes signature.
+EXPORTS = {
+    "gdr_chunk_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
+    "gdr_recurrent_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
+    "gdr_last_error": (ctypes.c_char_p, []),
+    "gdr_abi_version": (ctypes.c_int, []),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load_library(path: str = LIBRARY_PATH) -> ctypes.CDLL:
+    """Load libgdr.so once (after torch, so it binds to the HIP runtime torch already loaded)."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(path):
+                raise RuntimeError(
+                    f"libgdr.so not found at {path}; build it with `make -C {os.path.join(_HERE, 'csrc')}` "
+                    "(or __graft_entry__.build()).  There is no fallback implementation."
+                )
+            lib = ctypes.CDLL(path)
+            for name, (restype, argtypes) in EXPORTS.items():
+                fn = getattr(lib, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            if lib.gdr_abi_version() != ABI_VERSION:
+                raise RuntimeError(f"libgdr.so ABI {lib.gdr_abi_version()} != binding ABI {ABI_VERSION}; rebuild")
+            _lib = lib
+    return _lib
+
+
+def _view(x: torch.Tensor | None, name: str) -> GdrTensor:
+    view = GdrTensor()
+    if x is None:
+        return view
+    if x.dtype not in _DTYPE_CODES:
+        raise TypeError(f"{name}: unsupported dtype {x.dtype}")
+    if x.dim() == 4:
+        if x.shape[-1] > 1 and x.stride(-1) != 1:
+            raise ValueError(f"{name}: the last dimension must be contiguous")
+        sb, sh, st = x.stride(0), x.stride(1), x.stride(2)
+    elif x.dim() == 3:
+        sb, sh, st = x.stride(0), x.stride(1), x.stride(2)
+    else:
+        raise ValueError(f"{name}: expected 3 or 4 dimensions, got {tuple(x.shape)}")
+    view.ptr = x.data_ptr()
+    view.dtype = _DTYPE_CODES[x.dtype]
+    view.stride_b, view.stride_h, view.stride_t = sb, sh, st
+    return view
+
+
+def make_args(variant, q, k, v, gate, beta, out, scale, h0, ht, cu_seqlens=None) -> GdrArgs:
+    batch, heads, seq_len, key_dim = q.shape
+    args = GdrArgs()
+    args.abi_version = ABI_VERSION
+    args.variant = variant
+    args.batch, args.heads, args.seq_len, args.key_dim = batch, heads, seq_len, key_dim
+    args.value_dim = v.shape[-1]
+    args.scale = float(scale)
+    args.q, args.k, args.v = _view(q, "query"), _view(k, "key"), _view(v, "value")
+    args.gate, args.beta, args.out = _view(gate, "gate"), _view(beta, "beta"), _view(out, "out")
+    args.h0 = h0.data_ptr() if h0 is not None else None
+    args.ht = ht.data_ptr() if ht is not None else None
+    if cu_seqlens is not None:
+        args.cu_seqlens = cu_seqlens.data_ptr()
+        args.n_seqs = cu_seqlens.numel() - 1
+    return args
+
+
+def launch(entry: str, args: GdrArgs, device: torch.device) -> None:
+    lib = load_library()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    rc = getattr(lib, entry)(ctypes.byref(args), ctypes.c_void_p(stream))
+    if rc != 0:
+        raise RuntimeError(f"{entry} failed ({rc}): {lib.gdr_last_error().decode()}")

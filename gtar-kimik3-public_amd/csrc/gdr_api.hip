@@ -1,0 +1,113 @@
+// C-ABI entry points of libgdr.so: argument validation, error reporting and dispatch to the kernel launchers.
+// Nothing here allocates device memory; every launch goes to the caller's stream.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "gdr_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+bool valid_dtype(int d) { return d == GDR_F32 || d == GDR_BF16 || d == GDR_F16; }
+int elem_size(int d) { return d == GDR_F32 ? 4 : 2; }
+
+int check_view(const gdr_tensor& t, const char* name, bool required, bool f32_only) {
+  if (!t.ptr) return required ? fail(GDR_ERR_INVALID, "%s: null pointer", name) : GDR_OK;
+  if (!valid_dtype(t.dtype)) return fail(GDR_ERR_INVALID, "%s: unknown dtype code %d", name, t.dtype);
+  if (f32_only && t.dtype != GDR_F32) return fail(GDR_ERR_INVALID, "%s: must be float32", name);
+  if (t.stride_b < 0 || t.stride_h < 0 || t.stride_t < 0)
+    return fail(GDR_ERR_INVALID, "%s: negative strides are not supported", name);
+  return GDR_OK;
+}
+
+int check_common(const gdr_args* a, bool chunk) {
+  if (!a) return fail(GDR_ERR_INVALID, "args is NULL");
+  if (a->abi_version != GDR_ABI_VERSION)
+    return fail(GDR_ERR_INVALID, "abi_version %d, library implements %d", a->abi_version, GDR_ABI_VERSION);
+  if (a->variant < GDR_KDA || a->variant > GDR_DELTANET)
+    return fail(GDR_ERR_INVALID, "unknown variant %d", a->variant);
+  if (a->batch < 1 || a->heads < 1 || a->seq_len < 0)
+    return fail(GDR_ERR_INVALID, "bad sizes B=%d H=%d T=%d", a->batch, a->heads, a->seq_len);
+  if (a->key_dim != 64 && a->key_dim != 128)
+    return fail(GDR_ERR_UNSUPPORTED, "key dim %d not supported (64 or 128)", a->key_dim);
+  const int vmul = chunk ? 64 : 32;
+  if (a->value_dim < vmul || a->value_dim % vmul != 0 || a->value_dim > 1024)
+    return fail(GDR_ERR_UNSUPPORTED, "value dim %d not supported (a multiple of %d up to 1024)", a->value_dim,
+                vmul);
+  const bool has_gate = a->variant != GDR_DELTANET;
+  const bool has_beta = a->variant != GDR_GLA;
+  int rc;
+  if ((rc = check_view(a->q, "query", true, false))) return rc;
+  if ((rc = check_view(a->k, "key", true, false))) return rc;
+  if ((rc = check_view(a->v, "value", true, false))) return rc;
+  if ((rc = check_view(a->out, "out", true, false))) return rc;
+  if ((rc = check_view(a->gate, "gate", has_gate, true))) return rc;
+  if ((rc = check_view(a->beta, "beta", has_beta, true))) return rc;
+  if (!has_gate && a->gate.ptr) return fail(GDR_ERR_INVALID, "DeltaNet takes no gate");
+  if (!has_beta && a->beta.ptr) return fail(GDR_ERR_INVALID, "GLA takes no beta");
+  if ((reinterpret_cast<uintptr_t>(a->h0) | reinterpret_cast<uintptr_t>(a->ht)) % 16 != 0)
+    return fail(GDR_ERR_INVALID, "initial/final state must be 16-byte aligned");
+  if (a->cu_seqlens) {
+    if (!chunk) return fail(GDR_ERR_INVALID, "cu_seqlens is only accepted by the chunk mode");
+    if (a->batch != 1) return fail(GDR_ERR_INVALID, "cu_seqlens requires batch == 1 (got %d)", a->batch);
+    if (a->n_seqs < 1) return fail(GDR_ERR_INVALID, "cu_seqlens given with n_seqs=%d", a->n_seqs);
+  }
+  return GDR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gdr_abi_version(void) { return GDR_ABI_VERSION; }
+
+const char* gdr_last_error(void) { return g_last_error.c_str(); }
+
+int gdr_recurrent_fwd(const gdr_args* a, hipStream_t stream) {
+  int rc = check_common(a, false);
+  if (rc) return rc;
+  hipError_t e = gdr::launch_recurrent(*a, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "recurrent launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
+int gdr_chunk_fwd(const gdr_args* a, hipStream_t stream) {
+  int rc = check_common(a, true);
+  if (rc) return rc;
+  if (a->q.dtype != a->k.dtype || a->q.dtype != a->v.dtype)
+    return fail(GDR_ERR_INVALID, "chunk mode needs q, k, v of one dtype (got %d, %d, %d)", a->q.dtype,
+                a->k.dtype, a->v.dtype);
+  // Rows of q, k, v, gate and out are moved with 16-byte accesses.
+  const gdr_tensor* rows[] = {&a->q, &a->k, &a->v, &a->out, &a->gate};
+  const char* names[] = {"query", "key", "value", "out", "gate"};
+  for (int i = 0; i < 5; ++i) {
+    const gdr_tensor& t = *rows[i];
+    if (!t.ptr) continue;
+    if (i == 4 && a->variant == GDR_GDN) continue;  // scalar gate: element access
+    const int es = elem_size(t.dtype);
+    if (reinterpret_cast<uintptr_t>(t.ptr) % 16 || (t.stride_b * es) % 16 || (t.stride_h * es) % 16 ||
+        (t.stride_t * es) % 16)
+      return fail(GDR_ERR_INVALID, "%s: base pointer and b/h/t strides must be 16-byte aligned", names[i]);
+  }
+  hipError_t e = gdr::launch_chunk(*a, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "chunk launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
+}  // extern "C"

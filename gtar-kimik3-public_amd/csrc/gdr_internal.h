@@ -1,0 +1,16 @@
+// Host-side declarations shared between the C-ABI layer (gdr_api.hip) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/gdr.h"
+
+namespace gdr {
+
+// Enqueue the recurrent forward; `a` has been validated.
+hipError_t launch_recurrent(const gdr_args& a, hipStream_t stream);
+
+// Enqueue the chunkwise forward; `a` has been validated (q, k, v share one dtype).
+hipError_t launch_chunk(const gdr_args& a, hipStream_t stream);
+
+}  // namespace gdr

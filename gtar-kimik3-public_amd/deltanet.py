@@ -1,0 +1,43 @@
+"""DeltaNet (delta rule, no decay) on gfx950.
+
+    u_t = beta_t (v_t - k_t S_{t-1}),   S_t = S_{t-1} + k_t^T u_t,   o_t = scale q_t S_t
+
+Drop-in for src/ops/deltanet.py: `chunk_deltanet` (:406-420) and `recurrent_deltanet` (:423-445), same
+signatures (no gate) and conventions.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._common import run
+
+
+@torch.compiler.disable
+def chunk_deltanet(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    cu_seqlens: torch.Tensor | None = None,
+):
+    """Chunkwise (prefill) DeltaNet forward; `cu_seqlens` as in chunk_kimi_delta_attention."""
+    return run(_lib.DELTANET, True, query, key, value, None, beta, scale, initial_state, output_final_state,
+               cu_seqlens)
+
+
+def recurrent_deltanet(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+):
+    """Token-by-token (decode) DeltaNet forward."""
+    return run(_lib.DELTANET, False, query, key, value, None, beta, scale, initial_state, output_final_state)

@@ -1,0 +1,44 @@
+"""Gated DeltaNet (delta rule with a scalar per-head forget gate) on gfx950.
+
+    S_t = exp(g_t) S_{t-1},   u_t = beta_t (v_t - k_t S_t),   S_t = S_t + k_t^T u_t,   o_t = scale q_t S_t
+
+Drop-in for src/ops/gated_deltanet.py: `chunk_gated_deltanet` (:479-494) and `recurrent_gated_deltanet`
+(:497-520), same signatures and conventions.  gate and beta are (batch, heads, seq_len).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._common import run
+
+
+@torch.compiler.disable
+def chunk_gated_deltanet(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    gate: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    cu_seqlens: torch.Tensor | None = None,
+):
+    """Chunkwise (prefill) Gated DeltaNet forward; `cu_seqlens` as in chunk_kimi_delta_attention."""
+    return run(_lib.GDN, True, query, key, value, gate, beta, scale, initial_state, output_final_state, cu_seqlens)
+
+
+def recurrent_gated_deltanet(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    gate: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+):
+    """Token-by-token (decode) Gated DeltaNet forward."""
+    return run(_lib.GDN, False, query, key, value, gate, beta, scale, initial_state, output_final_state)

@@ -1,0 +1,42 @@
+"""Gated linear attention (per-channel forget gate, no delta rule) on gfx950.
+
+    S_t = diag(exp(g_t)) S_{t-1} + k_t^T v_t,   o_t = scale q_t S_t
+
+Drop-in for src/ops/gated_linear_attention.py: `chunk_gated_linear_attention` (:444-458) and
+`recurrent_gated_linear_attention` (:461-483), same signatures (no beta) and conventions.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._common import run
+
+
+@torch.compiler.disable
+def chunk_gated_linear_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    gate: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    cu_seqlens: torch.Tensor | None = None,
+):
+    """Chunkwise (prefill) GLA forward; `cu_seqlens` as in chunk_kimi_delta_attention."""
+    return run(_lib.GLA, True, query, key, value, gate, None, scale, initial_state, output_final_state, cu_seqlens)
+
+
+def recurrent_gated_linear_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    gate: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+):
+    """Token-by-token (decode) GLA forward."""
+    return run(_lib.GLA, False, query, key, value, gate, None, scale, initial_state, output_final_state)

@@ -1,0 +1,86 @@
+"""Seeded synthetic inputs for the benchmark configurations of this op family.
+
+The generators follow the input recipes attached to each configuration: q and k drawn N(0, 1) and
+L2-normalised along the key dimension, v ~ N(0, 1), beta = sigmoid(N(0, 1)) per (b, t, h), log-gates
+g = -softplus(N(0, 1)) (per channel for KDA and GLA, one per (b, t, h) for Gated DeltaNet), initial state
+~ N(0, sigma) or zero.  Tensors are drawn on the CPU from one `torch.Generator` in the layer's [B, T, H, D]
+order (as src/layers/kimi_delta_attention.py:41-49 produces them), moved to `device`, and returned in the op
+layout [B, H, T, D] -- as contiguous tensors, or as the layer's transposed views when `layer_layout` is set
+(src/layers/kimi_delta_attention.py:53), so both code paths of the strided loads get exercised.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import torch
+import torch.nn.functional as F
+
+GATES = {"kda": "channel", "gla": "channel", "gdn": "scalar", "deltanet": None}
+BETAS = {"kda": True, "gdn": True, "gla": False, "deltanet": True}
+
+
+@dataclasses.dataclass
+class Inputs:
+    query: torch.Tensor
+    key: torch.Tensor
+    value: torch.Tensor
+    gate: torch.Tensor | None
+    beta: torch.Tensor | None
+    initial_state: torch.Tensor | None
+
+    def args(self):
+        """Positional op arguments in the reference order for the variant (gate and beta only if it takes them)."""
+        return [x for x in (self.query, self.key, self.value, self.gate, self.beta) if x is not None]
+
+    def to(self, device):
+        move = lambda x: None if x is None else x.to(device)
+        return Inputs(*(move(x) for x in dataclasses.astuple(self)))
+
+
+def make_inputs(variant: str, batch: int, seq_len: int, heads: int, key_dim: int, value_dim: int, *,
+                seed: int = 0, dtype=torch.bfloat16, state_std: float | None = None, gate_scale: float = 1.0,
+                device="cpu", layer_layout: bool = False) -> Inputs:
+    """Draw one seeded input set.  `gate_scale` divides the log-gates (the reference tests' gate/16 ... gate/0.1
+    knob); `state_std` None means a zero (absent) initial state."""
+    gen = torch.Generator("cpu").manual_seed(seed)
+    shape_k = (batch, seq_len, heads, key_dim)
+    shape_v = (batch, seq_len, heads, value_dim)
+    query = F.normalize(torch.randn(shape_k, generator=gen), dim=-1).to(dtype)
+    key = F.normalize(torch.randn(shape_k, generator=gen), dim=-1).to(dtype)
+    value = torch.randn(shape_v, generator=gen).to(dtype)
+    gate = None
+    if GATES[variant] == "channel":
+        gate = -F.softplus(torch.randn(shape_k, generator=gen)) / gate_scale
+    elif GATES[variant] == "scalar":
+        gate = -F.softplus(torch.randn(batch, seq_len, heads, generator=gen)) / gate_scale
+    beta = torch.sigmoid(torch.randn(batch, seq_len, heads, generator=gen)) if BETAS[variant] else None
+    state = None
+    if state_std is not None:
+        state = torch.randn(batch, heads, key_dim, value_dim, generator=gen) * state_std
+
+    def place(x):
+        if x is None:
+            return None
+        x = x.to(device)
+        x = x.transpose(1, 2)
+        return x if layer_layout else x.contiguous()
+
+    return Inputs(place(query), place(key), place(value), place(gate), place(beta),
+                  None if state is None else state.to(device))
+
+
+def decode_inputs(variant: str, batch: int, heads: int, key_dim: int, value_dim: int, *, seed: int = 0,
+                  dtype=torch.bfloat16, device="cpu") -> Inputs:
+    """One decode token per sequence ([B, H, 1, D] views), without an initial state."""
+    return make_inputs(variant, batch, 1, heads, key_dim, value_dim, seed=seed, dtype=dtype, device=device)
+
+
+def decode_state(batch: int, heads: int, key_dim: int, value_dim: int, *, std: float = 0.02, seed: int = 0,
+                 device="cpu") -> torch.Tensor:
+    """fp32 decode state ~ N(0, std), drawn in slabs so a multi-GB state never needs a second host copy."""
+    gen = torch.Generator("cpu").manual_seed(seed)
+    out = torch.empty(batch, heads, key_dim, value_dim, dtype=torch.float32, device=device)
+    for b in range(batch):
+        out[b].copy_(torch.randn(heads, key_dim, value_dim, generator=gen) * std)
+    return out

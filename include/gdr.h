@@ -1,0 +1,106 @@
+/*
+ * gdr.h -- C ABI of the MI355X (gfx950) chunkwise gated delta-rule attention library (libgdr.so).
+ *
+ * One op family, four variants, two modes:
+ *   variant  KDA       S_t = diag(e^{g_t}) S_{t-1};  u_t = beta_t (v_t - k_t S_t);  S_t += k_t^T u_t;  o_t = scale q_t S_t
+ *            GDN       same with one scalar log-gate per (b, h, t)
+ *            GLA       S_t = diag(e^{g_t}) S_{t-1} + k_t^T v_t;  o_t = scale q_t S_t           (no beta, no delta rule)
+ *            DELTANET  KDA without decay                                                     (no gate)
+ *   mode     chunk     chunkwise-parallel prefill (WY form, chunk = 64 tokens)
+ *            recurrent token-by-token recurrence with the state in registers (decode, T = 1 typical)
+ *
+ * Layouts follow the reference op API: q, k [B, H, T, K]; v, o [B, H, T, V]; gate [B, H, T, K] (KDA, GLA) or
+ * [B, H, T] (GDN); beta [B, H, T]; states [N, H, K, V] fp32 row-major with V contiguous.  Every [B, H, T, D]
+ * operand is passed as a strided view (element strides for b, h, t; the last dimension must be contiguous),
+ * so transposed [B, T, H, D] storage needs no copy.
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers, allocated by the caller.  The library allocates nothing, keeps no
+ *     device memory between calls and never throws across this boundary.
+ *   - Work is enqueued asynchronously on `stream`; no entry point synchronises the device.
+ *   - Inputs are never written.  `h0` may alias `ht` (in-place state update); no other aliasing is allowed.
+ *   - Return value: GDR_OK (0), or a negative gdr_status.  gdr_last_error() returns a thread-local message
+ *     describing the last failure of the calling thread.
+ *   - Entry points are re-entrant and thread-safe.
+ */
+#ifndef GDR_H
+#define GDR_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDR_ABI_VERSION 1
+
+typedef enum gdr_variant { GDR_KDA = 0, GDR_GDN = 1, GDR_GLA = 2, GDR_DELTANET = 3 } gdr_variant;
+
+typedef enum gdr_dtype { GDR_F32 = 0, GDR_BF16 = 1, GDR_F16 = 2 } gdr_dtype;
+
+typedef enum gdr_status {
+  GDR_OK = 0,
+  GDR_ERR_INVALID = -1,     /* bad pointer, shape, stride, dtype or alignment */
+  GDR_ERR_UNSUPPORTED = -2, /* valid request this build does not implement (e.g. head dim 96) */
+  GDR_ERR_HIP = -3          /* a HIP runtime call failed (launch error) */
+} gdr_status;
+
+/* A strided [B, H, T, D] (or [B, H, T] for gate/beta of scalar-gated variants) view.  Strides in elements. */
+typedef struct gdr_tensor {
+  const void* ptr;
+  int32_t dtype; /* gdr_dtype */
+  int32_t reserved;
+  int64_t stride_b, stride_h, stride_t;
+} gdr_tensor;
+
+typedef struct gdr_args {
+  int32_t abi_version; /* must equal GDR_ABI_VERSION */
+  int32_t variant;     /* gdr_variant */
+  int32_t batch;       /* B; must be 1 when cu_seqlens is given */
+  int32_t heads;       /* H */
+  int32_t seq_len;     /* T (total packed length when cu_seqlens is given) */
+  int32_t key_dim;     /* K */
+  int32_t value_dim;   /* V */
+  float scale;         /* multiplies q; the Python layer resolves `scale or K**-0.5` */
+  gdr_tensor q, k, v;  /* q, k, v: bf16, f16 or f32 */
+  gdr_tensor gate;     /* f32; ptr NULL for DELTANET */
+  gdr_tensor beta;     /* f32; ptr NULL for GLA */
+  gdr_tensor out;      /* written; dtype bf16, f16 or f32 */
+  const float* h0;     /* [N, H, K, V] f32 contiguous, or NULL for a zero initial state */
+  float* ht;           /* [N, H, K, V] f32 contiguous, or NULL when the final state is not wanted */
+  const int32_t* cu_seqlens; /* device int32 [n_seqs + 1] packed-sequence offsets, or NULL */
+  int32_t n_seqs;            /* number of packed sequences (N); ignored when cu_seqlens is NULL (N = B) */
+  int32_t reserved;
+} gdr_args;
+
+/* Chunkwise forward (prefill).  Replaces, for all four variants, the forward of
+ *   ChunkKimiDeltaAttention     src/ops/kimi_delta_attention.py:535-558
+ *   ChunkGatedDeltaNet          src/ops/gated_deltanet.py:395-416
+ *   ChunkGatedLinearAttention   src/ops/gated_linear_attention.py:362-384
+ *   ChunkDeltaNet               src/ops/deltanet.py:326-347
+ * (pad_sequence + chunk_cumsum + kernel matrices + WY representation + state scan + output, six launches and
+ * a [B,H,NC+1,K,V] States buffer in the reference) with one fused launch.  q, k, v must share one dtype.
+ * Supports K in {64, 128}, V a multiple of 64, any T >= 1, and packed varlen input through cu_seqlens. */
+int gdr_chunk_fwd(const gdr_args* args, hipStream_t stream);
+
+/* Recurrent forward (decode).  Replaces the `_recurrent_forward` Triton launch of
+ *   recurrent_kimi_delta_attention     src/ops/kimi_delta_attention.py:666-692 (kernel :38-68)
+ *   recurrent_gated_deltanet           src/ops/gated_deltanet.py:497-520 (kernel :29-59)
+ *   recurrent_gated_linear_attention   src/ops/gated_linear_attention.py:461-483 (kernel :30-56)
+ *   recurrent_deltanet                 src/ops/deltanet.py:423-445 (kernel :30-57)
+ * Supports K in {64, 128}, V a multiple of 32, any T >= 1 (cu_seqlens must be NULL). */
+int gdr_recurrent_fwd(const gdr_args* args, hipStream_t stream);
+
+/* Thread-local description of the calling thread's last failure ("" if none).  No reference counterpart:
+ * the reference surfaces failures as Python exceptions raised by Triton. */
+const char* gdr_last_error(void);
+
+/* GDR_ABI_VERSION of the loaded library, so a binding can refuse a mismatched build. */
+int gdr_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDR_H */

@@ -1,0 +1,173 @@
+"""CPU oracle for the gated delta-rule attention family -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
+checker (or the timed CPU baseline).  The product path (the package's ops) never calls it: those run libgdr.so
+on the GPU and raise if it is missing.
+
+Contents, each a restatement in this repository's own torch code of the reference behaviour it cites:
+
+* `recurrence`      -- the token-by-token definition of all four variants, in any float dtype.
+                       KDA: src/ops/kimi_delta_attention.py:4 (math), :632-642 (`_reference`), and the fp64 test
+                       reference tests/test_kimi_delta_attention.py:24-35.  GDN: src/ops/gated_deltanet.py:1-5,
+                       tests/test_gated_deltanet.py:22-33.  GLA: src/ops/gated_linear_attention.py:1-3,
+                       tests/test_gated_linear_attention.py:23-31.  DeltaNet: src/ops/deltanet.py:1-6,
+                       tests/test_deltanet.py:21-31.  Unified gate-shape-agnostic form: tests/bench_ops.py:52-66.
+* `kda_reference`   -- the reference's CPU path for KDA exactly as the op runs it on CPU tensors: fp32 token loop
+                       with einsum, output cast to the value dtype, fp32 state
+                       (src/ops/kimi_delta_attention.py:632-642, dispatched at :659-660 and :679-681).  This is the
+                       "repo CPU reference" the benchmark times.
+* `chunkwise`       -- the chunkwise-parallel (WY / UT-transform) form of the same ops
+                       (src/ops/kimi_delta_attention.py:12-21, :535-558; gated_deltanet.py:11-14, :395-416;
+                       gated_linear_attention.py:9-13, :362-384; deltanet.py:12-16, :326-347), vectorised over
+                       (batch, head) with a Python loop over chunks, so full benchmark shapes finish in seconds.
+* `varlen`          -- packed variable-length input (`cu_seqlens`) as the concatenation of independent
+                       per-sequence runs.  The reference has no varlen path; this is the definition the kernel is
+                       held to.
+
+How each function is pinned (tests/test_oracle.py): closed forms (one-hot keys give an exact per-row
+overwrite / exponential-moving-average memory; beta = 0 gives pure decay of the initial state; GLA's
+non-recursive sum; DeltaNet with orthonormal keys and beta = 1 gives exact associative recall), the variant
+reductions (KDA with g = 0 is DeltaNet, KDA with channel-constant g is GDN, GLA with g = 0 is linear attention),
+chunkwise == recurrence at several chunk sizes, state passing between segments, causality, scale linearity and
+varlen == per-sequence runs.  No function is left "parity unpinned".
+
+Layouts follow the reference: q, k [B, H, T, K]; v [B, H, T, V]; gate [B, H, T, K] (KDA, GLA) or [B, H, T]
+(GDN); beta [B, H, T]; state [B, H, K, V].
+"""
+
+from __future__ import annotations
+
+import torch
+
+KDA, GDN, GLA, DELTANET = "kda", "gdn", "gla", "deltanet"
+VARIANTS = (KDA, GDN, GLA, DELTANET)
+
+
+def _decay_factor(variant, gate_t):
+    """exp(g_t) shaped to broadcast over the [B, H, K, V] state rows (None when the variant has no decay)."""
+    if variant in (KDA, GLA):
+        return gate_t.exp()[..., :, None]
+    if variant == GDN:
+        return gate_t.exp()[..., None, None]
+    return None
+
+
+def recurrence(variant, query, key, value, gate=None, beta=None, scale=None, initial_state=None,
+               dtype=torch.float64):
+    """Token recurrence in `dtype`; returns (o [B,H,T,V], final state [B,H,K,V]) both in `dtype`."""
+    scale = scale or query.shape[-1] ** -0.5
+    q, k, v = (x.to(dtype) for x in (query, key, value))
+    g = gate.to(dtype) if gate is not None else None
+    b = beta.to(dtype) if beta is not None else None
+    batch, heads, seq_len, key_dim = q.shape
+    state = (torch.zeros(batch, heads, key_dim, v.shape[-1], dtype=dtype) if initial_state is None
+             else initial_state.to(dtype).clone())
+    outputs = []
+    for t in range(seq_len):
+        decay = _decay_factor(variant, g[:, :, t]) if g is not None else None
+        if decay is not None:
+            state = state * decay
+        kt, vt = k[:, :, t], v[:, :, t]
+        if variant == GLA:
+            write = vt
+        else:
+            write = b[:, :, t, None] * (vt - torch.einsum("bhk,bhkv->bhv", kt, state))
+        state = state + kt[..., :, None] * write[..., None, :]
+        outputs.append(torch.einsum("bhk,bhkv->bhv", q[:, :, t] * scale, state))
+    out = torch.stack(outputs, 2) if outputs else v.new_zeros(v.shape)
+    return out, state
+
+
+def kda_reference(query, key, value, gate, beta, scale=None, initial_state=None):
+    """The reference op's CPU behaviour for KDA: fp32 loop, output in the value dtype, fp32 final state."""
+    scale = scale or query.shape[-1] ** -0.5
+    if initial_state is None:
+        initial_state = torch.zeros(query.shape[0], query.shape[1], query.shape[-1], value.shape[-1])
+    out, state = recurrence(KDA, query, key, value, gate, beta, scale, initial_state.float(), dtype=torch.float32)
+    return out.to(value.dtype), state
+
+
+def _chunk_log_decay(variant, g, start, end, key_dim):
+    """Within-chunk inclusive cumulative log decay b [B, H, C, K] (zeros for DeltaNet)."""
+    if variant in (KDA, GLA):
+        return g[:, :, start:end].cumsum(2)
+    if variant == GDN:
+        return g[:, :, start:end].cumsum(2)[..., None].expand(-1, -1, -1, key_dim)
+    return None
+
+
+def _pairwise_gated(left, key, b_chunk, strict):
+    """M[t, s] = sum_c left[t, c] key[s, c] exp(b[t, c] - b[s, c]) on the causal triangle (t > s or t >= s)."""
+    size = left.shape[2]
+    mask = torch.ones(size, size, dtype=torch.bool).tril(-1 if strict else 0)
+    if b_chunk is None:
+        return torch.where(mask, left @ key.transpose(-1, -2), 0.0)
+    span = (b_chunk[:, :, :1] - b_chunk[:, :, -1:]).abs().max().item()
+    if span < (600.0 if left.dtype == torch.float64 else 60.0):
+        # factorised around the mid-chunk cumulative decay: |exponent| stays far inside the float64 range
+        anchor = b_chunk[:, :, size // 2:size // 2 + 1]
+        lhs = left * (b_chunk - anchor).exp()
+        rhs = key * (anchor - b_chunk).exp()
+        return torch.where(mask, lhs @ rhs.transpose(-1, -2), 0.0)
+    # extreme gates: the exponent only ever enters as b_t - b_s <= 0 on the kept triangle
+    diff = b_chunk[:, :, :, None, :] - b_chunk[:, :, None, :, :]
+    diff = diff.masked_fill(~mask[:, :, None], float("-inf"))
+    return torch.einsum("bhtc,bhsc,bhtsc->bhts", left, key, diff.exp())
+
+
+def chunkwise(variant, query, key, value, gate=None, beta=None, scale=None, initial_state=None, chunk_size=64,
+              dtype=torch.float64):
+    """Chunkwise-parallel form.  Per chunk with state S entering it and b the in-chunk cumulative log decay:
+        P  = tril(K K^T (x) e^{b_t - b_s}, -1),   A = (I + diag(beta) P)^{-1}
+        u  = A diag(beta) (V - (K e^{b}) S)                      (GLA: u = V)
+        O  = (scale Q e^{b}) S + tril(scale Q K^T (x) e^{b_t - b_s}) u
+        S' = diag(e^{b_end}) S + (K e^{b_end - b})^T u
+    """
+    scale = scale or query.shape[-1] ** -0.5
+    q, k, v = (x.to(dtype) for x in (query, key, value))
+    g = gate.to(dtype) if gate is not None else None
+    b = beta.to(dtype) if beta is not None else None
+    batch, heads, seq_len, key_dim = q.shape
+    state = (torch.zeros(batch, heads, key_dim, v.shape[-1], dtype=dtype) if initial_state is None
+             else initial_state.to(dtype).clone())
+    out = torch.empty(batch, heads, seq_len, v.shape[-1], dtype=dtype)
+    for start in range(0, seq_len, chunk_size):
+        end = min(start + chunk_size, seq_len)
+        qc, kc, vc = q[:, :, start:end], k[:, :, start:end], v[:, :, start:end]
+        bc = _chunk_log_decay(variant, g, start, end, key_dim) if g is not None else None
+        if bc is None:
+            q_dec, k_dec, k_tail, chunk_decay = qc, kc, kc, None
+        else:
+            q_dec, k_dec = qc * bc.exp(), kc * bc.exp()
+            k_tail = kc * (bc[:, :, -1:] - bc).exp()
+            chunk_decay = bc[:, :, -1].exp()
+        if variant == GLA:
+            u = vc
+        else:
+            beta_c = b[:, :, start:end, None]
+            lower = beta_c * _pairwise_gated(kc, kc, bc, strict=True)
+            eye = torch.eye(end - start, dtype=dtype)
+            rhs = beta_c * (vc - k_dec @ state)
+            u = torch.linalg.solve_triangular(eye + lower, rhs, upper=False, unitriangular=True)
+        scores = scale * _pairwise_gated(qc, kc, bc, strict=False)
+        out[:, :, start:end] = (scale * q_dec) @ state + scores @ u
+        if chunk_decay is not None:
+            state = state * chunk_decay[..., None]
+        state = state + k_tail.transpose(-1, -2) @ u
+    return out, state
+
+
+def varlen(fn, variant, query, key, value, gate, beta, scale, initial_state, cu_seqlens, **kwargs):
+    """Packed sequences (batch 1, offsets `cu_seqlens`) as independent per-sequence runs, concatenated."""
+    offsets = [int(x) for x in cu_seqlens]
+    outs, states = [], []
+    for n in range(len(offsets) - 1):
+        s, e = offsets[n], offsets[n + 1]
+        sl = slice(s, e)
+        h0 = None if initial_state is None else initial_state[n:n + 1]
+        o, st = fn(variant, query[:, :, sl], key[:, :, sl], value[:, :, sl],
+                   None if gate is None else gate[:, :, sl], None if beta is None else beta[:, :, sl],
+                   scale, h0, **kwargs)
+        outs.append(o)
+        states.append(st)
+    return torch.cat(outs, 2), torch.cat(states, 0)

@@ -1,0 +1,118 @@
+"""The C-ABI boundary, checked without a GPU: libgdr.so loads, exports every symbol include/gdr.h declares,
+the ctypes structs match the header's layout byte for byte, and the Python layer rejects what the reference
+API would not accept before any device work is attempted."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from _helpers import ROOT, gdr, lib
+
+HEADER = os.path.join(ROOT, "include", "gdr.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(gdr_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    declared = _declared_functions()
+    assert declared == sorted(lib.EXPORTS), declared
+    so = lib.load_library()
+    for name in declared:
+        assert hasattr(so, name)
+    nm = subprocess.run(["nm", "-D", "--defined-only", lib.LIBRARY_PATH], capture_output=True, text=True,
+                        check=True).stdout
+    exported = set(re.findall(r" T (gdr_\w+)$", nm, flags=re.M))
+    assert exported == set(declared)
+    assert so.gdr_abi_version() == lib.ABI_VERSION
+
+
+def test_struct_layout_matches_header(tmp_path):
+    fields = [f for f, _ in lib.GdrArgs._fields_]
+    probe = tmp_path / "layout.c"
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {",
+             'printf("%zu %zu\\n", sizeof(gdr_args), sizeof(gdr_tensor));']
+    lines += [f'printf("{f} %zu\\n", offsetof(gdr_args, {f}));' for f in fields]
+    lines += [f'printf("t.{f} %zu\\n", offsetof(gdr_tensor, {f}));' for f, _ in lib.GdrTensor._fields_]
+    lines += ["return 0; }"]
+    probe.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", str(probe), "-o", str(exe)],
+                   check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    size_args, size_tensor = map(int, out[0].split())
+    assert size_args == ctypes.sizeof(lib.GdrArgs) and size_tensor == ctypes.sizeof(lib.GdrTensor)
+    offsets = dict(line.split() for line in out[1:] if line)
+    for f in fields:
+        assert int(offsets[f]) == getattr(lib.GdrArgs, f).offset, f
+    for f, _ in lib.GdrTensor._fields_:
+        assert int(offsets["t." + f]) == getattr(lib.GdrTensor, f).offset, f
+
+
+def test_last_error_reports_invalid_arguments_without_a_gpu():
+    so = lib.load_library()
+    args = lib.GdrArgs()
+    args.abi_version = lib.ABI_VERSION + 7
+    assert so.gdr_chunk_fwd(ctypes.byref(args), None) == -1
+    assert b"abi_version" in so.gdr_last_error()
+    args.abi_version = lib.ABI_VERSION
+    args.variant, args.batch, args.heads, args.seq_len, args.key_dim, args.value_dim = 0, 1, 1, 4, 96, 64
+    assert so.gdr_recurrent_fwd(ctypes.byref(args), None) == -2
+    assert b"key dim 96" in so.gdr_last_error()
+    args.key_dim = 64  # q is NULL
+    assert so.gdr_recurrent_fwd(ctypes.byref(args), None) == -1
+    assert b"query" in so.gdr_last_error()
+
+
+def _cpu_inputs():
+    q = torch.randn(1, 2, 8, 64)
+    return q, q.clone(), torch.randn(1, 2, 8, 64), -torch.rand(1, 2, 8, 64), torch.rand(1, 2, 8)
+
+
+def test_cpu_tensors_raise_instead_of_falling_back():
+    with pytest.raises(ValueError, match="GPU"):
+        gdr.chunk_kimi_delta_attention(*_cpu_inputs())
+    with pytest.raises(ValueError, match="GPU"):
+        gdr.recurrent_kimi_delta_attention(*_cpu_inputs())
+
+
+def test_gradients_are_refused():
+    q, k, v, g, b = _cpu_inputs()
+    q.requires_grad_()
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        gdr.chunk_kimi_delta_attention(q, k, v, g, b)
+
+
+def test_reference_export_surface():
+    names = {"chunk_kimi_delta_attention", "recurrent_kimi_delta_attention", "chunk_gated_deltanet",
+             "recurrent_gated_deltanet", "chunk_gated_linear_attention", "recurrent_gated_linear_attention",
+             "chunk_deltanet", "recurrent_deltanet"}
+    assert names <= set(dir(gdr))
+    import inspect
+    params = lambda f: list(inspect.signature(f).parameters)[:8]
+    assert params(gdr.chunk_kimi_delta_attention) == ["query", "key", "value", "gate", "beta", "scale",
+                                                       "initial_state", "output_final_state"]
+    assert params(gdr.chunk_gated_linear_attention)[:7] == ["query", "key", "value", "gate", "scale",
+                                                            "initial_state", "output_final_state"]
+    assert params(gdr.recurrent_deltanet) == ["query", "key", "value", "beta", "scale", "initial_state",
+                                              "output_final_state"]
+
+
+def test_recurrent_cache_fork_rollback_restores_state():
+    cache = gdr.RecurrentCache(2, 2, 4, 4, 8, 4, "cpu", torch.float32)
+    cache.update(torch.randn(2, 2, 4, 4), 3)
+    saved = cache.state.clone()
+    cache.fork()
+    cache.update(torch.randn(2, 2, 4, 4), 2)
+    cache.conv_states[0].fill_(5.0)
+    cache.rollback()
+    assert torch.equal(cache.state, saved) and cache.seq_len == 3
+    assert torch.count_nonzero(cache.conv_states[0]) == 0
+    with pytest.raises(RuntimeError):
+        cache.commit(1)

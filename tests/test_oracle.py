@@ -1,0 +1,200 @@
+"""Pins for the CPU oracle (oracle/gdr_oracle.py).  CPU only.
+
+Each test checks the oracle against something it does not share code with: closed forms that special inputs
+reduce the recurrence to, identities between variants, or a second algorithm (chunkwise vs token recurrence),
+chosen so that a plausible mistake -- decay on the value instead of the key dimension, a dropped or misplaced
+beta, a flipped error sign, reading the state before instead of after the decay, a wrong scale, an off-by-one
+in the cumulative gate -- fails at least one of them.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _helpers import oracle
+
+torch.set_default_dtype(torch.float64)
+
+
+def _rand_inputs(variant, B=2, H=2, T=12, K=4, V=3, seed=0, gate_scale=1.0, state=True):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, T, K, generator=gen)
+    k = F.normalize(torch.randn(B, H, T, K, generator=gen), dim=-1)
+    v = torch.randn(B, H, T, V, generator=gen)
+    g = None
+    if variant in ("kda", "gla"):
+        g = F.logsigmoid(torch.randn(B, H, T, K, generator=gen)) / gate_scale
+    elif variant == "gdn":
+        g = F.logsigmoid(torch.randn(B, H, T, generator=gen)) / gate_scale
+    beta = torch.sigmoid(torch.randn(B, H, T, generator=gen)) if variant != "gla" else None
+    h0 = torch.randn(B, H, K, V, generator=gen) if state else None
+    return q, k, v, g, beta, h0
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_one_hot_keys_reduce_to_per_row_memory(variant):
+    """With one-hot keys e_{c(t)} the state rows evolve independently: row c(t) becomes
+    (1 - beta) * decayed_row + beta * v_t (delta rule) or decayed_row + v_t (GLA); other rows only decay."""
+    B, H, T, K, V = 1, 1, 10, 5, 3
+    gen = torch.Generator().manual_seed(3)
+    slots = torch.randint(0, K, (T,), generator=gen)
+    k = F.one_hot(slots, K).double().view(1, 1, T, K)
+    q = torch.randn(B, H, T, K, generator=gen)
+    v = torch.randn(B, H, T, V, generator=gen)
+    h0 = torch.randn(B, H, K, V, generator=gen)
+    g = {"kda": -torch.rand(B, H, T, K, generator=gen), "gla": -torch.rand(B, H, T, K, generator=gen),
+         "gdn": -torch.rand(B, H, T, generator=gen), "deltanet": None}[variant]
+    beta = torch.rand(B, H, T, generator=gen) if variant != "gla" else None
+    scale = 0.7
+
+    rows = [h0[0, 0, c].clone() for c in range(K)]
+    expect_o = []
+    for t in range(T):
+        for c in range(K):
+            if g is not None:
+                rows[c] = rows[c] * math.exp(g[0, 0, t, c] if g.dim() == 4 else g[0, 0, t])
+        c = int(slots[t])
+        if variant == "gla":
+            rows[c] = rows[c] + v[0, 0, t]
+        else:
+            b = float(beta[0, 0, t])
+            rows[c] = (1.0 - b) * rows[c] + b * v[0, 0, t]
+        expect_o.append(scale * sum(float(q[0, 0, t, c]) * rows[c] for c in range(K)))
+    out, state = oracle.recurrence(variant, q, k, v, g, beta, scale, h0)
+    torch.testing.assert_close(out[0, 0], torch.stack(expect_o), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(state[0, 0], torch.stack(rows), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("variant", ["kda", "gdn"])
+def test_zero_beta_is_pure_decay_of_initial_state(variant):
+    """beta = 0 writes nothing: o_t = scale q_t diag(exp(sum_{s<=t} g_s)) S_0 and S_T = diag(exp(sum g)) S_0."""
+    q, k, v, g, beta, h0 = _rand_inputs(variant, T=9)
+    beta = torch.zeros_like(beta)
+    out, state = oracle.recurrence(variant, q, k, v, g, beta, 0.5, h0)
+    cum = g.cumsum(2)
+    if variant == "gdn":
+        cum = cum[..., None].expand(-1, -1, -1, q.shape[-1])
+    expect = 0.5 * torch.einsum("bhtk,bhkv->bhtv", q * cum.exp(), h0)
+    torch.testing.assert_close(out, expect, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(state, h0 * cum[:, :, -1, :, None].exp(), rtol=1e-12, atol=1e-12)
+
+
+def test_gla_matches_non_recursive_sum():
+    """GLA state is an explicit decayed sum: S_t = diag(e^{b_t}) S_0 + sum_{s<=t} diag(e^{b_t - b_s}) k_s^T v_s."""
+    q, k, v, g, _, h0 = _rand_inputs("gla", T=7)
+    out, state = oracle.recurrence("gla", q, k, v, g, None, 0.3, h0)
+    cum = g.cumsum(2)
+    T = q.shape[2]
+    for t in range(T):
+        s_t = h0 * cum[:, :, t, :, None].exp()
+        for s in range(t + 1):
+            decay = (cum[:, :, t] - cum[:, :, s]).exp()
+            s_t = s_t + (decay * k[:, :, s])[..., :, None] * v[:, :, s, None, :]
+        torch.testing.assert_close(out[:, :, t], 0.3 * torch.einsum("bhk,bhkv->bhv", q[:, :, t], s_t))
+    torch.testing.assert_close(state, s_t)
+
+
+def test_deltanet_orthonormal_keys_give_exact_recall_and_overwrite():
+    """beta = 1 with orthonormal keys stores (key -> value) pairs exactly; writing a key again overwrites it."""
+    K, V = 6, 4
+    gen = torch.Generator().manual_seed(5)
+    basis, _ = torch.linalg.qr(torch.randn(K, K, generator=gen))
+    order = [0, 1, 2, 0, 3]  # key 0 is written twice
+    k = torch.stack([basis[:, i] for i in order]).view(1, 1, len(order), K)
+    v = torch.randn(1, 1, len(order), V, generator=gen)
+    q = k.clone()
+    beta = torch.ones(1, 1, len(order))
+    out, state = oracle.recurrence("deltanet", q, k, v, None, beta, 1.0, None)
+    latest = {}
+    for t, key_id in enumerate(order):
+        latest[key_id] = v[0, 0, t]
+        torch.testing.assert_close(out[0, 0, t], latest[key_id], rtol=1e-10, atol=1e-10)
+    expect = sum(basis[:, i][:, None] * latest[i][None, :] for i in latest)
+    torch.testing.assert_close(state[0, 0], expect, rtol=1e-10, atol=1e-10)
+
+
+def test_variant_reductions():
+    """KDA with g = 0 is DeltaNet; KDA with a channel-constant gate is GDN; GLA with g = 0 is linear attention."""
+    q, k, v, g, beta, h0 = _rand_inputs("kda", T=11)
+    delta = oracle.recurrence("deltanet", q, k, v, None, beta, None, h0)
+    kda0 = oracle.recurrence("kda", q, k, v, torch.zeros_like(g), beta, None, h0)
+    for a, b in zip(delta, kda0):
+        torch.testing.assert_close(a, b)
+    scalar_gate = g[..., 0]
+    gdn = oracle.recurrence("gdn", q, k, v, scalar_gate, beta, None, h0)
+    kda_c = oracle.recurrence("kda", q, k, v, scalar_gate[..., None].expand_as(g), beta, None, h0)
+    for a, b in zip(gdn, kda_c):
+        torch.testing.assert_close(a, b)
+    gla0, _ = oracle.recurrence("gla", q, k, v, torch.zeros_like(g), None, 0.25, h0)
+    scores = torch.einsum("bhtk,bhsk->bhts", q, k).tril()
+    linear = 0.25 * (scores @ v + q @ h0)
+    torch.testing.assert_close(gla0, linear)
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+@pytest.mark.parametrize("chunk_size", [16, 32, 64])
+@pytest.mark.parametrize("gate_scale", [16.0, 1.0, 0.1])
+def test_chunkwise_equals_recurrence(variant, chunk_size, gate_scale):
+    """The WY/UT chunkwise algorithm and the token recurrence agree (T = 100 exercises a partial last chunk,
+    gate_scale 0.1 the extreme-decay branch)."""
+    q, k, v, g, beta, h0 = _rand_inputs(variant, B=1, H=2, T=100, K=8, V=5, gate_scale=gate_scale)
+    ref = oracle.recurrence(variant, q, k, v, g, beta, None, h0)
+    got = oracle.chunkwise(variant, q, k, v, g, beta, None, h0, chunk_size=chunk_size)
+    for a, b in zip(got, ref):
+        torch.testing.assert_close(a, b, rtol=1e-9, atol=1e-9)
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_state_passing_and_causality(variant):
+    q, k, v, g, beta, h0 = _rand_inputs(variant, T=16)
+    full_o, full_s = oracle.recurrence(variant, q, k, v, g, beta, None, h0)
+    cut = lambda x, sl: None if x is None else x[:, :, sl]
+    first = slice(0, 7)
+    second = slice(7, 16)
+    _, mid = oracle.recurrence(variant, *(cut(x, first) for x in (q, k, v, g, beta)), None, h0)
+    o2, s2 = oracle.recurrence(variant, *(cut(x, second) for x in (q, k, v, g, beta)), None, mid)
+    torch.testing.assert_close(o2, full_o[:, :, 7:])
+    torch.testing.assert_close(s2, full_s)
+    v2 = v.clone()
+    v2[:, :, 9:] += 1.0
+    o_pert, _ = oracle.recurrence(variant, q, k, v2, g, beta, None, h0)
+    torch.testing.assert_close(o_pert[:, :, :9], full_o[:, :, :9], rtol=0, atol=0)
+    assert (o_pert[:, :, 9:] - full_o[:, :, 9:]).abs().max() > 1e-3
+
+
+def test_scale_is_linear_and_default_is_inverse_sqrt_dim():
+    q, k, v, g, beta, h0 = _rand_inputs("kda", K=16, T=5)
+    o1, _ = oracle.recurrence("kda", q, k, v, g, beta, 0.5, h0)
+    o2, _ = oracle.recurrence("kda", q, k, v, g, beta, 1.0, h0)
+    od, _ = oracle.recurrence("kda", q, k, v, g, beta, None, h0)
+    torch.testing.assert_close(2 * o1, o2)
+    torch.testing.assert_close(od, o2 * 0.25)
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_varlen_is_per_sequence(variant):
+    q, k, v, g, beta, _ = _rand_inputs(variant, B=1, H=2, T=40, state=False)
+    cu = torch.tensor([0, 5, 23, 40])
+    gen = torch.Generator().manual_seed(9)
+    h0 = torch.randn(3, 2, q.shape[-1], v.shape[-1], generator=gen)
+    o, s = oracle.varlen(oracle.chunkwise, variant, q, k, v, g, beta, None, h0, cu, chunk_size=16)
+    for n in range(3):
+        a, e = int(cu[n]), int(cu[n + 1])
+        cut = lambda x: None if x is None else x[:, :, a:e]
+        ro, rs = oracle.recurrence(variant, *(cut(x) for x in (q, k, v, g, beta)), None, h0[n:n + 1])
+        torch.testing.assert_close(o[:, :, a:e], ro)
+        torch.testing.assert_close(s[n:n + 1], rs)
+
+
+def test_kda_reference_dtype_contract():
+    """The reference CPU path returns the output in the value dtype and an fp32 state."""
+    q, k, v, g, beta, h0 = _rand_inputs("kda", T=6)
+    out, state = oracle.kda_reference(q.bfloat16(), k.bfloat16(), v.bfloat16(), g.float(), beta.float(), None,
+                                      h0.float())
+    assert out.dtype == torch.bfloat16 and state.dtype == torch.float32
+    ref_o, ref_s = oracle.recurrence("kda", q.bfloat16(), k.bfloat16(), v.bfloat16(), g.float(), beta.float(),
+                                     None, h0.float())
+    assert (out.double() - ref_o).abs().max() <= 1e-2 * ref_o.abs().max()
+    assert (state.double() - ref_s).norm() <= 1e-5 * ref_s.norm()
