@@ -1,7 +1,623 @@
-// Chunkwise forward: placeholder until the fused kernel lands.
+// Chunkwise (prefill) forward of the gated delta-rule family on gfx950: one fused launch.
+//
+// Reference: the forward of ChunkKimiDeltaAttention (src/ops/kimi_delta_attention.py:535-558), which runs
+// chunk_cumsum (utils.py:15-23), two kernel-matrix launches (:71-106), the WY representation (:109-136), the
+// sequential state scan (:139-170) and the output kernel (:173-197), materialising gate_cumsum, P, scores, A,
+// W, U, u and a [B, H, NC+1, K, V] States tensor in HBM.  Gated DeltaNet, GLA and DeltaNet are the same chunk
+// algebra with a scalar gate, no delta rule, or no gate (gated_deltanet.py:62-162, gated_linear_attention.py:
+// 59-144, deltanet.py:60-149).
+//
+// Algebra per chunk of C = 64 tokens with state S entering it (b = in-chunk inclusive cumsum of the log gate):
+//   P  = tril(K K^T (x) e^{b_t - b_s}, -1),  L = diag(beta) P,  A = (I + L)^{-1}
+//   u  = A diag(beta) (V - (K e^b) S)                  (GLA: u = V)
+//   O  = (scale Q e^b) S + tril(scale Q K^T (x) e^{b_t - b_s}) u
+//   S' = diag(e^{b_end}) S + (K e^{b_end - b})^T u
+// which is the reference's  W = A beta K e^b,  U = A beta V,  u = U - W S  with the product W S regrouped so W
+// is never formed.
+//
+// MI355X design:
+//   * One workgroup = one (sequence, head) x one 64-column value slice; 4 waves, wave w owns 16 state columns.
+//     The fp32 state slice [K, 16] of each wave lives in MFMA accumulator layout in registers for the whole
+//     sequence: it is read from HBM once (h0) and written once (ht).  No per-chunk state ever reaches HBM.
+//   * Per chunk, each wave first prepares one 16-row block: loads q, k (bf16) and the gate, forms the in-block
+//     cumulative gate, and writes every MFMA operand to LDS in bf16 with its decay factor folded in.  Decay
+//     factors are anchored per 16-row block so that every factor that multiplies an off-diagonal operand is
+//     <= 1 (the reference's secondary chunking, kimi_delta_attention.py:84-100, done with one anchor per query
+//     block instead of one per block pair).  Diagonal 16x16 blocks use the block-start anchor, whose key factor
+//     e^{-b} is bounded by the block's own decay span; channels whose span exceeds kHotSpan fall back to an
+//     exact elementwise evaluation (the reference always evaluates diagonal blocks elementwise, utils.py:48-53).
+//   * Gated K K^T and Q K^T strips are bf16 MFMA (v_mfma_f32_16x16x32_bf16).  The 16x16 diagonal blocks of
+//     A are inverted in fp32 by forward substitution; the off-diagonal part of the WY solve is a blocked forward
+//     substitution on MFMA (v_mfma_f32_16x16x16_bf16) straight from accumulator registers, so neither A nor u
+//     touches LDS.  The state readout, the K S product and the state update are MFMA with the state operand
+//     taken directly from the accumulator registers (the accumulator row layout of two 16-row tiles is a valid
+//     k-slot layout for the 16x16x32 operand when the other operand uses the same k permutation).
+//   * Output tiles are staged in LDS and written with 16-byte stores.
 #include "gdr_common.h"
 #include "gdr_internal.h"
 
 namespace gdr {
-hipError_t launch_chunk(const gdr_args&, hipStream_t) { return hipErrorNotSupported; }
+
+namespace {
+
+constexpr int kChunk = 64;      // tokens per chunk
+constexpr int kSlice = 64;      // value columns per workgroup (4 waves x 16)
+constexpr float kHotSpan = 60.f;  // a channel whose 16-row decay span exceeds this is handled elementwise
+
+__device__ __forceinline__ floatx4 mfma32(bf16x8 a, bf16x8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx4 mfma16(bf16x4 a, bf16x4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ __bf16 bf(float x) { return static_cast<__bf16>(x); }
+__device__ __forceinline__ float f32(__bf16 x) { return static_cast<float>(x); }
+__device__ __forceinline__ bf16x4 pack4(floatx4 v) { return bf16x4{bf(v[0]), bf(v[1]), bf(v[2]), bf(v[3])}; }
+__device__ __forceinline__ bf16x8 concat(bf16x4 lo, bf16x4 hi) {
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+__device__ __forceinline__ void unpack8(uint4 raw, float* out) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void store8(__bf16* dst, const float* v, float s) {
+  bf16x8 p;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) p[i] = bf(v[i] * s);
+  *reinterpret_cast<bf16x8*>(dst) = p;
+}
+
+template <typename OutT>
+__device__ __forceinline__ void store_row16(OutT* dst, const float* src);
+template <>
+__device__ __forceinline__ void store_row16<__bf16>(__bf16* dst, const float* src) {
+  bf16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = bf(src[i]);
+    b[i] = bf(src[8 + i]);
+  }
+  reinterpret_cast<bf16x8*>(dst)[0] = a;
+  reinterpret_cast<bf16x8*>(dst)[1] = b;
+}
+template <>
+__device__ __forceinline__ void store_row16<_Float16>(_Float16* dst, const float* src) {
+  typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+  f16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = static_cast<_Float16>(src[i]);
+    b[i] = static_cast<_Float16>(src[8 + i]);
+  }
+  reinterpret_cast<f16x8*>(dst)[0] = a;
+  reinterpret_cast<f16x8*>(dst)[1] = b;
+}
+template <>
+__device__ __forceinline__ void store_row16<float>(float* dst, const float* src) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    reinterpret_cast<float4*>(dst)[i] = make_float4(src[4 * i], src[4 * i + 1], src[4 * i + 2], src[4 * i + 3]);
+}
+
+// LDS map (element offsets into one __bf16 array; fp32 regions are carved out at the end).
+template <int K>
+struct Lds {
+  static constexpr int KP = K + 8;        // pitch of [64][K] bf16 operand arrays (16-byte skew per row)
+  static constexpr int TP = kChunk + 8;   // pitch of [*][64] bf16 arrays
+  // Region U1, prep phase: Lq, Lk, Rd [64][KP]; Kap [48][KP] (key blocks 0..2, end-anchored);
+  // Far [48][KP] (key blocks scaled for tiles (2,0), (3,0), (3,1)).
+  static constexpr int Lq = 0, Lk = Lq + 64 * KP, Rd = Lk + 64 * KP, Kap = Rd + 64 * KP, Far = Kap + 48 * KP;
+  static constexpr int U1_END = Far + 48 * KP;
+  // Region U2 overlays U1 in the column phase: Qt, Kh [64][KP]; KtT [K][TP].
+  static constexpr int Qt = 0, Kh = Qt + 64 * KP, KtT = Kh + 64 * KP;
+  static constexpr int U2_END = KtT + K * TP;
+  static_assert(U2_END <= U1_END, "column-phase operands must fit in the prep region");
+  static constexpr int Sc = U1_END;           // [64][TP] bf16 gated scores (lower block triangle)
+  static constexpr int NegL = Sc + 64 * TP;   // [64][TP] bf16 -L (off-diagonal blocks)
+  static constexpr int Ainv = NegL + 64 * TP; // [4][16][16] bf16 diagonal-block inverses
+  static constexpr int Vt = Ainv + 4 * 256;   // [64][TP] bf16 value tile of the slice
+  static constexpr int BF16_END = Vt + 64 * TP;
+  // fp32 regions (float offsets from the byte offset 2 * BF16_END, rounded up to 16 bytes)
+  static constexpr int F0 = ((2 * BF16_END + 15) / 16) * 4;
+  static constexpr int Lii = F0;                  // [4][16][17] fp32 strictly-lower diagonal blocks of L
+  static constexpr int Ostg = Lii + 4 * 16 * 17;  // [64][68] fp32 output staging
+  static constexpr int Beta = Ostg + 64 * 68;     // [64]
+  static constexpr int Tot = Beta + 64;           // [4][K] block totals of the log gate
+  static constexpr int Gam = Tot + 4 * K;         // [K] e^{b_end}
+  static constexpr int Hot = Gam + K;             // [4] per-block "has a hot channel" flags
+  static constexpr int F_END = Hot + 4;
+  static constexpr int BYTES = F_END * 4;
+};
+
+}  // namespace
+
+template <int VARIANT, int K, typename OutT>
+__global__ __launch_bounds__(256, 1) void chunk_fwd_kernel(const gdr_args a, int n_slices, int xcd_map) {
+  constexpr bool kDelta = VARIANT != GDR_GLA;
+  constexpr int kGate = (VARIANT == GDR_KDA || VARIANT == GDR_GLA) ? 2 : (VARIANT == GDR_GDN ? 1 : 0);
+  constexpr int LPR = K / 8;       // prep lanes per row (8 channels each)
+  constexpr int RSG = kWave / LPR; // row subgroups per wave
+  constexpr int RPL = 16 / RSG;    // rows per prep lane
+  constexpr int KT = K / 16;       // 16-channel tiles of the state
+  constexpr int KS = K / 32;       // k-steps of 32 channels
+  using M = Lds<K>;
+  constexpr int KP = M::KP, TP = M::TP;
+
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  __bf16* sb = reinterpret_cast<__bf16*>(smem_raw);
+  float* sf = reinterpret_cast<float*>(smem_raw);
+
+  // ---- workgroup -> (sequence, head, value slice); XCD-aware so the slices of one head share an L2 ----
+  const int x = blockIdx.x;
+  int bh, slice;
+  if (xcd_map) {
+    const int xcd = x & 7, local = x >> 3;
+    slice = local % n_slices;
+    bh = (local / n_slices) * 8 + xcd;
+  } else {
+    slice = x % n_slices;
+    bh = x / n_slices;
+  }
+  const int H = a.heads, V = a.value_dim;
+  const int n = bh / H, h = bh % H;
+  int bos = 0, len = a.seq_len, bidx = n;
+  if (a.cu_seqlens) {
+    const int lo = min(max(a.cu_seqlens[n], 0), a.seq_len);
+    const int hi = min(max(a.cu_seqlens[n + 1], lo), a.seq_len);
+    bos = lo;
+    len = hi - lo;
+    bidx = 0;
+  }
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int v0 = slice * kSlice;
+  const int col = v0 + 16 * wave + l16;  // this lane's state/output column in the column phase
+
+  const __bf16* qp = static_cast<const __bf16*>(a.q.ptr) + bidx * a.q.stride_b + h * a.q.stride_h +
+                     int64_t(bos) * a.q.stride_t;
+  const __bf16* kp = static_cast<const __bf16*>(a.k.ptr) + bidx * a.k.stride_b + h * a.k.stride_h +
+                     int64_t(bos) * a.k.stride_t;
+  const __bf16* vp = static_cast<const __bf16*>(a.v.ptr) + bidx * a.v.stride_b + h * a.v.stride_h +
+                     int64_t(bos) * a.v.stride_t;
+  const float* gp = kGate ? static_cast<const float*>(a.gate.ptr) + bidx * a.gate.stride_b +
+                                h * a.gate.stride_h + int64_t(bos) * a.gate.stride_t
+                          : nullptr;
+  const float* betap = kDelta ? static_cast<const float*>(a.beta.ptr) + bidx * a.beta.stride_b +
+                                    h * a.beta.stride_h + int64_t(bos) * a.beta.stride_t
+                              : nullptr;
+  OutT* op = static_cast<OutT*>(const_cast<void*>(a.out.ptr)) + bidx * a.out.stride_b + h * a.out.stride_h +
+             int64_t(bos) * a.out.stride_t;
+  const size_t sbase = size_t(n * H + h) * K * V;
+
+  // ---- state slice in accumulator layout: st[m][i] = S[16 m + 4 g4 + i][col] ----
+  floatx4 st[KT];
+#pragma unroll
+  for (int m = 0; m < KT; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st[m][i] = a.h0 ? a.h0[sbase + size_t(16 * m + 4 * g4 + i) * V + col] : 0.f;
+
+  // prep-lane geometry: lane holds rows 16 wave + rs * RPL + j (j < RPL), channels c0 .. c0 + 7
+  const int cg = lane % LPR, rs = lane / LPR, c0 = 8 * cg;
+  const float scale = a.scale;
+  const int nchunks = (len + kChunk - 1) / kChunk;
+
+  for (int ci = 0; ci < nchunks; ++ci) {
+    const int t0 = ci * kChunk;
+    // =========================== step a: loads and in-block gate prefix ===========================
+    float qf[RPL][8], kf[RPL][8], bl[RPL][8];
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) {
+      const int t = t0 + 16 * wave + rs * RPL + j;
+      if (t < len) {
+        unpack8(*reinterpret_cast<const uint4*>(qp + t * a.q.stride_t + c0), qf[j]);
+        unpack8(*reinterpret_cast<const uint4*>(kp + t * a.k.stride_t + c0), kf[j]);
+        if constexpr (kGate == 2) {
+          const float4 g0 = *reinterpret_cast<const float4*>(gp + t * a.gate.stride_t + c0);
+          const float4 g1 = *reinterpret_cast<const float4*>(gp + t * a.gate.stride_t + c0 + 4);
+          bl[j][0] = g0.x; bl[j][1] = g0.y; bl[j][2] = g0.z; bl[j][3] = g0.w;
+          bl[j][4] = g1.x; bl[j][5] = g1.y; bl[j][6] = g1.z; bl[j][7] = g1.w;
+        } else if constexpr (kGate == 1) {
+          const float g = gp[t * a.gate.stride_t];
+#pragma unroll
+          for (int c = 0; c < 8; ++c) bl[j][c] = g;
+        } else {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) bl[j][c] = 0.f;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) qf[j][c] = kf[j][c] = bl[j][c] = 0.f;
+      }
+    }
+    if constexpr (kGate) {
+#pragma unroll
+      for (int j = 1; j < RPL; ++j)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) bl[j][c] += bl[j - 1][c];
+      // inclusive scan of the lane totals over the RSG lanes that share this channel group
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float tot = bl[RPL - 1][c];
+        float incl = tot;
+#pragma unroll
+        for (int off = LPR; off < kWave; off *= 2) {
+          const float y = __shfl_up(incl, off, kWave);
+          if (lane >= off) incl += y;
+        }
+        const float excl = incl - tot;
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) bl[j][c] += excl;
+      }
+      if (rs == RSG - 1) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) sf[M::Tot + wave * K + c0 + c] = bl[RPL - 1][c];
+      }
+    }
+    // value tile of the slice and beta
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int chunk16 = tid + 256 * r;  // 512 pieces of 8 bf16
+      const int row = chunk16 >> 3, cc = (chunk16 & 7) * 8;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (t0 + row < len) val = *reinterpret_cast<const uint4*>(vp + (t0 + row) * a.v.stride_t + v0 + cc);
+      *reinterpret_cast<uint4*>(sb + M::Vt + row * TP + cc) = val;
+    }
+    if (tid < kChunk) {
+      float bv = 0.f;
+      if constexpr (kDelta) {
+        if (t0 + tid < len) bv = betap[(t0 + tid) * a.beta.stride_t];
+      }
+      sf[M::Beta + tid] = bv;
+    }
+    __syncthreads();
+
+    // =========================== step b: decay factors and prep-phase operands ===========================
+    float ea_prev[8], eb_tail[8], tw[8], far1[8], far2[8];
+    bool hot[8];
+    bool any_hot = false;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      ea_prev[c] = eb_tail[c] = far1[c] = far2[c] = 1.f;
+      tw[c] = 0.f;
+      hot[c] = false;
+    }
+    if constexpr (kGate) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float tb[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) tb[m] = sf[M::Tot + m * K + c0 + c];
+        float prev = 0.f, tail = 0.f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          if (m < wave) prev += tb[m];
+          if (m > wave) tail += tb[m];
+        }
+        tw[c] = tb[wave];
+        ea_prev[c] = exp_fast(prev);
+        eb_tail[c] = exp_fast(tail);
+        hot[c] = -tw[c] > kHotSpan;
+        any_hot |= hot[c];
+        // far-tile scalings: wave 0 -> tiles (2,0) e^{T1} and (3,0) e^{T1+T2}; wave 1 -> tile (3,1) e^{T2}
+        far1[c] = exp_fast(wave == 0 ? tb[1] : tb[2]);
+        far2[c] = exp_fast(tb[1] + tb[2]);
+        if (wave == 0 && rs == 0) sf[M::Gam + c0 + c] = exp_fast(tb[0] + tb[1] + tb[2] + tb[3]);
+      }
+    } else {
+      if (wave == 0 && rs == 0) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) sf[M::Gam + c0 + c] = 1.f;
+      }
+    }
+    float ell[RPL][8], rho[RPL][8];
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) {
+      const int tl = 16 * wave + rs * RPL + j;  // chunk-local row
+      float rd[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        if constexpr (kGate) {
+          ell[j][c] = exp_fast(bl[j][c]);
+          rho[j][c] = exp_fast(tw[c] - bl[j][c]);
+          rd[c] = hot[c] ? 0.f : kf[j][c] * exp_fast(-bl[j][c]);
+        } else {
+          ell[j][c] = rho[j][c] = 1.f;
+          rd[c] = kf[j][c];
+        }
+      }
+      float lq[8], lk[8], kap[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        lq[c] = qf[j][c] * ell[j][c];
+        lk[c] = kf[j][c] * ell[j][c];
+        kap[c] = kf[j][c] * rho[j][c];
+      }
+      store8(sb + M::Lq + tl * KP + c0, lq, scale);
+      store8(sb + M::Lk + tl * KP + c0, lk, 1.f);
+      store8(sb + M::Rd + tl * KP + c0, rd, 1.f);
+      if (wave < 3) store8(sb + M::Kap + tl * KP + c0, kap, 1.f);
+      if (wave < 2) {
+        float f1[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) f1[c] = kap[c] * far1[c];
+        // Far rows: [0,16) tile (2,0), [16,32) tile (3,0), [32,48) tile (3,1)
+        if (wave == 0) {
+          float f2[8];
+#pragma unroll
+          for (int c = 0; c < 8; ++c) f2[c] = kap[c] * far2[c];
+          store8(sb + M::Far + tl * KP + c0, f1, 1.f);
+          store8(sb + M::Far + (16 + tl) * KP + c0, f2, 1.f);
+        } else {
+          store8(sb + M::Far + (32 + tl - 16) * KP + c0, f1, 1.f);
+        }
+      }
+    }
+    if constexpr (kGate) {
+      const bool wave_hot = __any(any_hot);
+      if (lane == 0) sf[M::Hot + wave] = wave_hot ? 1.f : 0.f;
+    }
+    __syncthreads();
+
+    // =========================== step c: gated score / kernel-matrix strips (wave w: query block w) ============
+    for (int j = 0; j <= wave; ++j) {
+      int key_off;
+      if (j == wave) key_off = M::Rd + 16 * j * KP;
+      else if (j == wave - 1) key_off = M::Kap + 16 * j * KP;
+      else if (wave == 2) key_off = M::Far;             // (2,0)
+      else if (j == 0) key_off = M::Far + 16 * KP;      // (3,0)
+      else key_off = M::Far + 32 * KP;                  // (3,1)
+      floatx4 acc_s = {0.f, 0.f, 0.f, 0.f}, acc_p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const int kc = 32 * kk + 8 * g4;
+        const bf16x8 bk = *reinterpret_cast<const bf16x8*>(sb + key_off + l16 * KP + kc);
+        const bf16x8 aq = *reinterpret_cast<const bf16x8*>(sb + M::Lq + (16 * wave + l16) * KP + kc);
+        acc_s = mfma32(aq, bk, acc_s);
+        if constexpr (kDelta) {
+          const bf16x8 ak = *reinterpret_cast<const bf16x8*>(sb + M::Lk + (16 * wave + l16) * KP + kc);
+          acc_p = mfma32(ak, bk, acc_p);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tloc = 4 * g4 + i, sloc = l16;
+        const int row = 16 * wave + tloc;
+        float s = acc_s[i];
+        if (j == wave && tloc < sloc) s = 0.f;
+        sb[M::Sc + row * TP + 16 * j + sloc] = bf(s);
+        if constexpr (kDelta) {
+          const float p = acc_p[i] * sf[M::Beta + row];
+          if (j < wave) sb[M::NegL + row * TP + 16 * j + sloc] = bf(-p);
+          else sf[M::Lii + wave * 272 + tloc * 17 + sloc] = tloc > sloc ? p : 0.f;
+        }
+      }
+    }
+    __syncthreads();
+
+    // exact elementwise diagonal blocks for channels whose in-block decay span is too large for a factorisation
+    if constexpr (kGate) {
+      if (sf[M::Hot + wave] != 0.f) {
+        for (int s = 0; s < 16; ++s) {
+          const int src = cg + LPR * (s / RPL);
+          const int js = s % RPL;
+          float ks[8], bs[8];
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            float kv = 0.f, bv = 0.f;
+#pragma unroll
+            for (int jj = 0; jj < RPL; ++jj) {
+              if (jj == js) {
+                kv = kf[jj][c];
+                bv = bl[jj][c];
+              }
+            }
+            ks[c] = __shfl(kv, src, kWave);
+            bs[c] = __shfl(bv, src, kWave);
+          }
+#pragma unroll
+          for (int j = 0; j < RPL; ++j) {
+            const int t = rs * RPL + j;
+            float p = 0.f, sc = 0.f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+              if (hot[c]) {
+                const float d = exp_fast(fminf(bl[j][c] - bs[c], 0.f));
+                p += kf[j][c] * ks[c] * d;
+                sc += qf[j][c] * ks[c] * d;
+              }
+            }
+#pragma unroll
+            for (int m = 1; m < LPR; m *= 2) {
+              p += shfl_xor(p, m);
+              sc += shfl_xor(sc, m);
+            }
+            if (cg == 0 && t >= s) {
+              const int row = 16 * wave + t;
+              __bf16* dst = sb + M::Sc + row * TP + 16 * wave + s;
+              *dst = bf(f32(*dst) + scale * sc);
+              if (kDelta && t > s) sf[M::Lii + wave * 272 + t * 17 + s] += sf[M::Beta + row] * p;
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+    // =========================== step d: column-phase operands (overlay U1) and diagonal inverses ===========
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) {
+      const int tl = 16 * wave + rs * RPL + j;
+      float qt[8], kh[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        qt[c] = qf[j][c] * ell[j][c] * ea_prev[c];
+        kh[c] = kf[j][c] * ell[j][c] * ea_prev[c];
+      }
+      store8(sb + M::Qt + tl * KP + c0, qt, scale);
+      store8(sb + M::Kh + tl * KP + c0, kh, 1.f);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int tl0 = 16 * wave + rs * RPL;
+#pragma unroll
+      for (int j = 0; j < RPL; ++j)
+        sb[M::KtT + (c0 + c) * TP + tl0 + j] = bf(kf[j][c] * rho[j][c] * eb_tail[c]);
+    }
+    if constexpr (kDelta) {
+      if (lane < 16) {  // column `lane` of (I + L_ww)^{-1}, forward substitution in fp32
+        const float* Lw = sf + M::Lii + wave * 272;
+        float xcol[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float acc = (r == lane) ? 1.f : 0.f;
+#pragma unroll
+          for (int m = 0; m < r; ++m) acc -= Lw[r * 17 + m] * xcol[m];
+          xcol[r] = acc;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sb[M::Ainv + wave * 256 + r * 16 + lane] = bf(xcol[r]);
+      }
+    }
+    __syncthreads();
+
+    // =========================== step e: column work (wave w: 16 value columns) ===========================
+    bf16x8 sB[KS];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) sB[kk] = concat(pack4(st[2 * kk]), pack4(st[2 * kk + 1]));
+    floatx4 acc_o[4], yv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      floatx4 ax = {0.f, 0.f, 0.f, 0.f}, ao = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const int r0 = (16 * i + l16) * KP + 32 * kk + 4 * g4;
+        const bf16x8 ak = concat(*reinterpret_cast<const bf16x4*>(sb + M::Kh + r0),
+                                 *reinterpret_cast<const bf16x4*>(sb + M::Kh + r0 + 16));
+        const bf16x8 aq = concat(*reinterpret_cast<const bf16x4*>(sb + M::Qt + r0),
+                                 *reinterpret_cast<const bf16x4*>(sb + M::Qt + r0 + 16));
+        if constexpr (kDelta) ax = mfma32(ak, sB[kk], ax);
+        ao = mfma32(aq, sB[kk], ao);
+      }
+      acc_o[i] = ao;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int row = 16 * i + 4 * g4 + jj;
+        const float vv = f32(sb[M::Vt + row * TP + 16 * wave + l16]);
+        yv[i][jj] = kDelta ? sf[M::Beta + row] * (vv - ax[jj]) : vv;
+      }
+    }
+    bf16x4 ub[4];
+    if constexpr (kDelta) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        floatx4 z = yv[i];
+#pragma unroll
+        for (int j = 0; j < i; ++j) {
+          const bf16x4 nl =
+              *reinterpret_cast<const bf16x4*>(sb + M::NegL + (16 * i + l16) * TP + 16 * j + 4 * g4);
+          z = mfma16(nl, ub[j], z);
+        }
+        const bf16x4 ai = *reinterpret_cast<const bf16x4*>(sb + M::Ainv + i * 256 + l16 * 16 + 4 * g4);
+        const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+        ub[i] = pack4(mfma16(ai, pack4(z), zero));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ub[i] = pack4(yv[i]);
+    }
+    // intra-chunk output
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j <= i; ++j) {
+        const bf16x4 sc = *reinterpret_cast<const bf16x4*>(sb + M::Sc + (16 * i + l16) * TP + 16 * j + 4 * g4);
+        acc_o[i] = mfma16(sc, ub[j], acc_o[i]);
+      }
+    }
+    // state update  S = diag(gamma) S + Kt^T u
+#pragma unroll
+    for (int m = 0; m < KT; ++m) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st[m][i] *= sf[M::Gam + 16 * m + 4 * g4 + i];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int r0 = (16 * m + l16) * TP + 32 * kk + 4 * g4;
+        const bf16x8 ak = concat(*reinterpret_cast<const bf16x4*>(sb + M::KtT + r0),
+                                 *reinterpret_cast<const bf16x4*>(sb + M::KtT + r0 + 16));
+        st[m] = mfma32(ak, concat(ub[2 * kk], ub[2 * kk + 1]), st[m]);
+      }
+    }
+    // stage the output tile, then write full rows
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) sf[M::Ostg + (16 * i + 4 * g4 + jj) * 68 + 16 * wave + l16] = acc_o[i][jj];
+    __syncthreads();
+    {
+      const int row = tid >> 2, cc = (tid & 3) * 16;
+      if (t0 + row < len) store_row16<OutT>(op + (t0 + row) * a.out.stride_t + v0 + cc, sf + M::Ostg + row * 68 + cc);
+    }
+    __syncthreads();
+  }
+
+  if (a.ht) {
+#pragma unroll
+    for (int m = 0; m < KT; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a.ht[sbase + size_t(16 * m + 4 * g4 + i) * V + col] = st[m][i];
+  }
+}
+
+namespace {
+
+template <int VARIANT, int K, typename OutT>
+hipError_t launch_typed(const gdr_args& a, hipStream_t stream) {
+  const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
+  const int bh = n_seq * a.heads;
+  const int n_slices = a.value_dim / kSlice;
+  const int xcd_map = (bh % 8 == 0) ? 1 : 0;
+  constexpr int bytes = Lds<K>::BYTES;
+  static bool configured = false;  // benign race: every thread sets the same attribute
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_fwd_kernel<VARIANT, K, OutT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  hipLaunchKernelGGL((chunk_fwd_kernel<VARIANT, K, OutT>), dim3(bh * n_slices), dim3(256), bytes, stream, a,
+                     n_slices, xcd_map);
+  return hipGetLastError();
+}
+
+template <int VARIANT, int K>
+hipError_t launch_k(const gdr_args& a, hipStream_t stream) {
+  switch (a.out.dtype) {
+    case GDR_BF16: return launch_typed<VARIANT, K, __bf16>(a, stream);
+    case GDR_F16: return launch_typed<VARIANT, K, _Float16>(a, stream);
+    default: return launch_typed<VARIANT, K, float>(a, stream);
+  }
+}
+
+template <int VARIANT>
+hipError_t launch_v(const gdr_args& a, hipStream_t stream) {
+  return a.key_dim == 64 ? launch_k<VARIANT, 64>(a, stream) : launch_k<VARIANT, 128>(a, stream);
+}
+
+}  // namespace
+
+hipError_t launch_chunk(const gdr_args& a, hipStream_t stream) {
+  if (a.q.dtype != GDR_BF16) return hipErrorInvalidValue;  // the Python layer converts q, k, v to bf16
+  switch (a.variant) {
+    case GDR_KDA: return launch_v<GDR_KDA>(a, stream);
+    case GDR_GDN: return launch_v<GDR_GDN>(a, stream);
+    case GDR_GLA: return launch_v<GDR_GLA>(a, stream);
+    default: return launch_v<GDR_DELTANET>(a, stream);
+  }
+}
+
 }  // namespace gdr

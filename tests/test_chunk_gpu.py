@@ -1,0 +1,143 @@
+"""Parity of the fused chunkwise (prefill) HIP kernel against the oracle, through the reference op API.
+
+Tolerance (bf16 q/k/v in, fp32 state): out max-abs error <= 2e-2 * max|o_ref| and final-state relative Frobenius
+error <= 1e-2, against the fp64 oracle on the same bf16-rounded inputs.  Cases follow the reference tests'
+grid (src tests/test_kimi_delta_attention.py:107-114 and the per-variant equivalents): head dims 64/128,
+T not a multiple of 64, gate scales 16 / 1 / 0.1 (the last one drives every diagonal block down the exact
+elementwise path), correlated keys, random initial states, plus the benchmark shapes, the layer's transposed
+layout, packed varlen input and state passing.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _helpers import CHUNK_FNS, OUT_TOL, RECURRENT_FNS, STATE_TOL, oracle, oracle_args, out_error, \
+    state_error, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(variant, inp, **kw):
+    with torch.no_grad():
+        return CHUNK_FNS[variant](*inp.args(), initial_state=inp.initial_state, output_final_state=True, **kw)
+
+
+def _check(variant, inp, label, **kw):
+    out, state = _run(variant, inp, **kw)
+    torch.cuda.synchronize()
+    q, k, v, g, beta, h0 = oracle_args(inp)
+    ref_o, ref_s = oracle.chunkwise(variant, q, k, v, g, beta, None, h0)
+    eo, es = out_error(out, ref_o), state_error(state, ref_s)
+    print(f"{label}: out err {eo:.2e} state err {es:.2e}", flush=True)
+    assert out.dtype == inp.value.dtype and state.dtype == torch.float32
+    assert torch.isfinite(out.float()).all() and torch.isfinite(state).all()
+    assert eo <= OUT_TOL and es <= STATE_TOL, (eo, es)
+    return out, state
+
+
+CASES = [
+    # (B, H, T, K, V, gate_scale, state_std)
+    (1, 2, 64, 64, 64, 1.0, None),
+    (2, 4, 256, 64, 64, 16.0, 1.0),
+    (2, 4, 256, 64, 64, 1.0, 1.0),
+    (2, 4, 256, 128, 64, 16.0, 1.0),
+    (1, 2, 200, 64, 128, 4.0, 1.0),
+    (2, 2, 512, 128, 128, 16.0, 1.0),
+    (2, 4, 256, 64, 64, 0.1, 1.0),
+    (1, 2, 1, 128, 128, 1.0, 0.02),
+    (1, 3, 65, 128, 128, 1.0, 0.02),
+    (3, 2, 130, 128, 192, 1.0, 0.02),
+]
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "B{}H{}T{}K{}V{}g{}".format(*c[:6]))
+def test_chunk_matches_oracle(variant, case):
+    B, H, T, K, V, gate_scale, state_std = case
+    inp = workloads.make_inputs(variant, B, T, H, K, V, seed=0, gate_scale=gate_scale, state_std=state_std,
+                                device="cuda")
+    _check(variant, inp, f"chunk {variant} {case}")
+
+
+@pytest.mark.parametrize("variant", ["kda", "gdn", "deltanet"])
+def test_chunk_correlated_keys(variant):
+    """Consecutive keys nearly parallel (reference tests' `correlated` mode): the WY solve is ill-conditioned."""
+    B, H, T, K, V = 2, 4, 256, 128, 128
+    inp = workloads.make_inputs(variant, B, T, H, K, V, seed=4, state_std=1.0, device="cuda")
+    gen = torch.Generator().manual_seed(11)
+    base = torch.randn(B, H, 1, K, generator=gen)
+    key = F.normalize(base + 0.2 * torch.randn(B, H, T, K, generator=gen), dim=-1)
+    inp.key = key.to(torch.bfloat16).cuda()
+    _check(variant, inp, f"chunk {variant} correlated")
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_chunk_layer_layout_and_fp32_output(variant):
+    """Transposed [B,T,H,D] views (what the KDA layer passes) and an fp32 value dtype."""
+    inp = workloads.make_inputs(variant, 2, 150, 4, 128, 128, seed=5, state_std=0.02, device="cuda",
+                                layer_layout=True)
+    assert not inp.query.is_contiguous()
+    _check(variant, inp, f"chunk {variant} layer layout")
+    inp.value = inp.value.float()
+    _check(variant, inp, f"chunk {variant} fp32 value")
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_chunk_state_passing(variant):
+    """Two halves with the state carried equal one call (reference tests' check_state_passing)."""
+    inp = workloads.make_inputs(variant, 2, 256, 2, 64, 64, seed=1, state_std=0.5, device="cuda")
+    full_o, full_s = _run(variant, inp)
+    half = 100
+    cut = lambda x, sl: None if x is None else x[:, :, sl]
+    first = workloads.Inputs(*(cut(x, slice(0, half)) for x in (inp.query, inp.key, inp.value, inp.gate,
+                                                                  inp.beta)), inp.initial_state)
+    _, mid = _run(variant, first)
+    second = workloads.Inputs(*(cut(x, slice(half, 256)) for x in (inp.query, inp.key, inp.value, inp.gate,
+                                                                     inp.beta)), mid)
+    o2, s2 = _run(variant, second)
+    assert (o2.float() - full_o[:, :, half:].float()).abs().max().item() < 5e-2
+    assert state_error(s2, full_s) < 1e-2
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_chunk_varlen_matches_per_sequence(variant):
+    lens = [1, 64, 65, 200, 37, 128]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    total = int(cu[-1])
+    H, K, V = 2, 128, 128
+    inp = workloads.make_inputs(variant, 1, total, H, K, V, seed=7, device="cuda")
+    gen = torch.Generator().manual_seed(8)
+    h0 = torch.randn(len(lens), H, K, V, generator=gen) * 0.1
+    with torch.no_grad():
+        out, state = CHUNK_FNS[variant](*inp.args(), initial_state=h0.cuda(), output_final_state=True,
+                                        cu_seqlens=cu.cuda())
+    q, k, v, g, beta, _ = oracle_args(inp)
+    ref_o, ref_s = oracle.varlen(oracle.chunkwise, variant, q, k, v, g, beta, None, h0, cu)
+    eo, es = out_error(out, ref_o), state_error(state, ref_s)
+    print(f"varlen {variant}: out err {eo:.2e} state err {es:.2e}", flush=True)
+    assert eo <= OUT_TOL and es <= STATE_TOL
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_chunk_agrees_with_recurrent_kernel(variant):
+    inp = workloads.make_inputs(variant, 2, 300, 2, 128, 128, seed=9, state_std=0.02, device="cuda")
+    co, cs = _run(variant, inp)
+    with torch.no_grad():
+        ro, rs = RECURRENT_FNS[variant](*inp.args(), initial_state=inp.initial_state, output_final_state=True)
+    assert out_error(co, ro.double()) <= OUT_TOL and state_error(cs, rs.double()) <= STATE_TOL
+
+
+def test_chunk_prefill_config_full_size():
+    """Benchmark prefill shape: B=4, T=4096, H=16, d=128, h0 ~ N(0, 0.02)."""
+    print("chunk kda B=4 T=4096 H=16 K=V=128", flush=True)
+    inp = workloads.make_inputs("kda", 4, 4096, 16, 128, 128, seed=0, state_std=0.02, device="cuda")
+    _check("kda", inp, "chunk kda full size")
+
+
+@pytest.mark.parametrize("variant", ["gdn", "gla", "deltanet"])
+def test_chunk_variant_sweep_full_size(variant):
+    """Variant sweep shape: B=2, T=8192, H=16, d=128, zero initial state."""
+    print(f"chunk {variant} B=2 T=8192 H=16 K=V=128", flush=True)
+    inp = workloads.make_inputs(variant, 2, 8192, 16, 128, 128, seed=0, device="cuda")
+    _check(variant, inp, f"chunk {variant} full size")
