@@ -1,0 +1,207 @@
+"""Benchmark of the gfx950 gated delta-rule kernels on the headline configurations.
+
+One JSON line on stdout:
+  * value / ms_per_step: KDA chunkwise prefill at B=4, T=4096, H=16, dk=dv=128, chunk 64 (bf16 q/k/v, fp32
+    per-channel gate, beta and state, initial state ~ N(0, 0.02)); one step = one call of
+    chunk_kimi_delta_attention(..., output_final_state=True) with every input already resident in HBM.
+  * roofline: the fused chunk kernel against HBM (its bound): algorithmic bytes per launch (inputs read once,
+    outputs written once) / average launch time measured with HIP events on the launch stream; traffic = HBM
+    bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary when it matches the current
+    kernel source, else null.  mfma_frac reports the same launch against the dense bf16 MFMA peak.
+  * decode: the batch-256 KDA decode step (fp32 state [256,16,128,128] ~ N(0, 0.02), one token per sequence,
+    1000 back-to-back steps, state handed from step to step as the reference API does), in state GB/s.
+  * cpu_baseline: the reference's CPU path for the op (fp32 token loop, restated in oracle/) timed on this
+    host on a bounded sample of the same prefill workload.
+Only one GPU is used; --gpus above 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import hashlib
+import importlib
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PREFILL = dict(B=4, T=4096, H=16, K=128, V=128, chunk=64)
+DECODE = dict(B=256, H=16, K=128, V=128, steps=1000)
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "chunk_kda_prefill_traffic.json")
+
+
+def delta_flops_per_token_head(C, K, V):
+    """Causal FLOP count of the chunkwise delta rule per token and head: P, W and scores C*K each; U and the
+    intra-chunk output C*V each; W S, K^T u and Q S 2*K*V each; the triangular inverse C^2/3."""
+    return C * (3 * K + 2 * V) + 6 * K * V + C * C / 3
+
+
+def prefill_bytes(B, T, H, K, V, **_):
+    bf16, f32 = 2, 4
+    reads = B * T * H * (2 * K * bf16 + V * bf16 + K * f32 + f32) + B * H * K * V * f32
+    writes = B * T * H * V * bf16 + B * H * K * V * f32
+    return reads + writes
+
+
+def decode_bytes(B, H, K, V, **_):
+    bf16, f32 = 2, 4
+    state = 2 * B * H * K * V * f32
+    io = B * H * (2 * K * bf16 + V * bf16 + K * f32 + f32 + V * bf16)
+    return state + io
+
+
+def source_hash():
+    path = os.path.join(ROOT, "gtar-kimik3-public_amd", "csrc", "chunk.hip")
+    return hashlib.sha256(open(path, "rb").read()).hexdigest()[:16]
+
+
+def committed_traffic():
+    try:
+        summary = json.load(open(TRAFFIC_SUMMARY))
+    except (OSError, ValueError):
+        return None
+    if summary.get("chunk_hip_sha256_16") != source_hash():
+        return None
+    return summary.get("hbm_bytes_per_launch")
+
+
+def bench_prefill(gdr, workloads, torch, steps, warmup):
+    cfg = PREFILL
+    dev = torch.device("cuda")
+    inp = workloads.make_inputs("kda", cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"], seed=0, state_std=0.02,
+                                device=dev)
+    args = inp.args()
+
+    def step():
+        return gdr.chunk_kimi_delta_attention(*args, initial_state=inp.initial_state, output_final_state=True)
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            step()
+        stop.record(stream)
+        torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms per step (= per launch: one kernel per call)
+
+
+def bench_decode(gdr, workloads, torch, warmup):
+    cfg = DECODE
+    dev = torch.device("cuda")
+    ring = [workloads.decode_inputs("kda", cfg["B"], cfg["H"], cfg["K"], cfg["V"], seed=100 + i, device=dev)
+            for i in range(8)]
+    state = workloads.decode_state(cfg["B"], cfg["H"], cfg["K"], cfg["V"], std=0.02, seed=7, device=dev)
+
+    def run(n, state):
+        for i in range(n):
+            r = ring[i % 8]
+            _, state = gdr.recurrent_kimi_delta_attention(*r.args(), initial_state=state, output_final_state=True)
+        return state
+
+    with torch.no_grad():
+        state = run(warmup, state)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        state = run(cfg["steps"], state)
+        stop.record(stream)
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / cfg["steps"]
+    gbs = decode_bytes(**cfg) / (ms * 1e-3) / 1e9
+    return {"workload": "kda_decode_step", "B": cfg["B"], "H": cfg["H"], "K": cfg["K"], "V": cfg["V"],
+            "steps": cfg["steps"], "us_per_step": round(ms * 1e3, 3), "value": round(gbs, 1),
+            "unit": "GB/s (state + io bytes per step)", "tokens_per_s": round(cfg["B"] / (ms * 1e-3), 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+
+
+def cpu_baseline(workloads, torch, budget_s):
+    """The reference CPU path (fp32 token loop) on the full prefill workload, repeated until `budget_s`."""
+    from oracle import gdr_oracle as oracle
+
+    cfg = PREFILL
+    inp = workloads.make_inputs("kda", cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"], seed=0, state_std=0.02)
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        oracle.kda_reference(inp.query, inp.key, inp.value, inp.gate, inp.beta, None, inp.initial_state)
+        passes += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= budget_s:
+            break
+    tokens = passes * cfg["B"] * cfg["T"]
+    return {"value": round(tokens / elapsed, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{passes} full pass(es) of the prefill workload (B=4 T=4096 H=16 dk=dv=128) through the "
+                      f"reference's fp32 CPU token loop, {elapsed:.1f} s, {len(os.sched_getaffinity(0))} host "
+                      "cores visible"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="minimum seconds of CPU baseline work")
+    opts = ap.parse_args()
+    if opts.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this op family runs per (sequence, head) with no cross-GPU "
+              "exchange, and multi-GPU runs are out of scope for this build.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    gdr = importlib.import_module("gtar-kimik3-public_amd")
+    workloads = importlib.import_module("gtar-kimik3-public_amd.workloads")
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+
+    ms = bench_prefill(gdr, workloads, torch, opts.steps, opts.warmup)
+    cfg = PREFILL
+    tokens = cfg["B"] * cfg["T"]
+    nbytes = prefill_bytes(**cfg)
+    flops = delta_flops_per_token_head(cfg["chunk"], cfg["K"], cfg["V"]) * tokens * cfg["H"]
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    tflops = flops / (ms * 1e-3) / 1e12
+    record = {
+        "metric": "KDA prefill tokens/sec (% MFMA peak); decode-step state GB/s (% HBM peak)",
+        "value": round(tokens / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": opts.steps,
+        "warmup": opts.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "kda_chunk_prefill", **cfg, "state": "fp32", "gate": "fp32 per-channel"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": committed_traffic()},
+        "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+        "tflops": round(tflops, 2),
+        "algorithmic_bytes": nbytes,
+        "algorithmic_flops": flops,
+    }
+    if not opts.no_decode:
+        record["decode"] = bench_decode(gdr, workloads, torch, warmup=20)
+    if not opts.no_cpu:
+        record["cpu_baseline"] = cpu_baseline(workloads, torch, opts.cpu_budget)
+    print(json.dumps(record), flush=True)
+
+
+if __name__ == "__main__":
+    main()

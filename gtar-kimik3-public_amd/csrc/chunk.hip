@@ -15,24 +15,27 @@
 // which is the reference's  W = A beta K e^b,  U = A beta V,  u = U - W S  with the product W S regrouped so W
 // is never formed.
 //
-// MI355X design:
-//   * One workgroup = one (sequence, head) x one 64-column value slice; 4 waves, wave w owns 16 state columns.
-//     The fp32 state slice [K, 16] of each wave lives in MFMA accumulator layout in registers for the whole
-//     sequence: it is read from HBM once (h0) and written once (ht).  No per-chunk state ever reaches HBM.
-//   * Per chunk, each wave first prepares one 16-row block: loads q, k (bf16) and the gate, forms the in-block
-//     cumulative gate, and writes every MFMA operand to LDS in bf16 with its decay factor folded in.  Decay
-//     factors are anchored per 16-row block so that every factor that multiplies an off-diagonal operand is
-//     <= 1 (the reference's secondary chunking, kimi_delta_attention.py:84-100, done with one anchor per query
-//     block instead of one per block pair).  Diagonal 16x16 blocks use the block-start anchor, whose key factor
-//     e^{-b} is bounded by the block's own decay span; channels whose span exceeds kHotSpan fall back to an
-//     exact elementwise evaluation (the reference always evaluates diagonal blocks elementwise, utils.py:48-53).
-//   * Gated K K^T and Q K^T strips are bf16 MFMA (v_mfma_f32_16x16x32_bf16).  The 16x16 diagonal blocks of
-//     A are inverted in fp32 by forward substitution; the off-diagonal part of the WY solve is a blocked forward
-//     substitution on MFMA (v_mfma_f32_16x16x16_bf16) straight from accumulator registers, so neither A nor u
-//     touches LDS.  The state readout, the K S product and the state update are MFMA with the state operand
-//     taken directly from the accumulator registers (the accumulator row layout of two 16-row tiles is a valid
-//     k-slot layout for the 16x16x32 operand when the other operand uses the same k permutation).
-//   * Output tiles are staged in LDS and written with 16-byte stores.
+// MI355X design (one launch; one workgroup per (sequence, head) x 64-column value slice; 8 waves):
+//   * Waves 4-7 are producers, waves 0-3 consumers, and the two groups run one chunk apart: in step s the
+//     producers prepare chunk s while the consumers run the state recurrence of chunk s-1, so the VALU-heavy
+//     preparation (gate cumsum, decay factors, operand scaling) overlaps the MFMA-heavy state chain on every
+//     SIMD.  The only per-step workgroup barrier sits between steps; operands pass through a double-buffered
+//     LDS region, and the producers hand off among themselves through an LDS counter.  Global loads of the
+//     next chunk are issued a step ahead.
+//   * Producer wave p owns the 16-row block p of a chunk.  Decay factors are anchored per 16-row block so that
+//     every factor folded into an off-diagonal operand is <= 1 (the reference's secondary chunking,
+//     kimi_delta_attention.py:84-100, with one anchor per query block instead of one per block pair).  Diagonal
+//     blocks use the block-start anchor, whose key factor e^{-b} is bounded by the block's own decay span;
+//     channels whose span exceeds kHotSpan are evaluated exactly elementwise instead (the reference always
+//     evaluates diagonal blocks elementwise, utils.py:48-53).  Gated K K^T and Q K^T strips run on bf16 MFMA
+//     (v_mfma_f32_16x16x32_bf16); each producer inverts its 16x16 diagonal block of (I + diag(beta) P) in
+//     fp32 and stores it with the off-diagonal -diag(beta) P blocks.
+//   * Consumer wave w owns 16 state columns as an fp32 [K, 16] accumulator tile in registers for the whole
+//     sequence (read from h0 once, written to ht once; no per-chunk state touches HBM).  K S and the Q S
+//     readout take the state straight from the accumulator registers as the MFMA B operand (two accumulator
+//     tiles form one 32-deep k slot set when the A operand is read with the same k permutation); the WY solve
+//     is a blocked forward substitution on v_mfma_f32_16x16x16_bf16 from registers; the state update reads
+//     (K e^{b_end - b})^T with the gfx950 transposing LDS read (ds_read_b64_tr_b16) from the row-major tile.
 #include "gdr_common.h"
 #include "gdr_internal.h"
 
@@ -63,6 +66,10 @@ __device__ __forceinline__ void unpack8(uint4 raw, float* out) {
     out[2 * i] = __uint_as_float(w[i] << 16);
     out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
   }
+}
+__device__ __forceinline__ float bf16_elem(uint4 raw, int c) {
+  const uint32_t w = c < 2 ? raw.x : c < 4 ? raw.y : c < 6 ? raw.z : raw.w;
+  return __uint_as_float((c & 1) ? (w & 0xffff0000u) : (w << 16));
 }
 __device__ __forceinline__ void store8(__bf16* dst, const float* v, float s) {
   bf16x8 p;
@@ -103,53 +110,153 @@ __device__ __forceinline__ void store_row16<float>(float* dst, const float* src)
     reinterpret_cast<float4*>(dst)[i] = make_float4(src[4 * i], src[4 * i + 1], src[4 * i + 2], src[4 * i + 3]);
 }
 
-// LDS map (element offsets into one __bf16 array; fp32 regions are carved out at the end).
+// LDS map.  Two consumer buffers (one per chunk parity) followed by the producer-private region.  Offsets of
+// bf16 arrays are in elements from the buffer base; everything else is in bytes from the LDS base.
 template <int K>
 struct Lds {
-  static constexpr int KP = K + 8;        // pitch of [64][K] bf16 operand arrays (16-byte skew per row)
-  static constexpr int TP = kChunk + 8;   // pitch of [*][64] bf16 arrays
-  // Region U1, prep phase: Lq, Lk, Rd [64][KP]; Kap [48][KP] (key blocks 0..2, end-anchored);
-  // Far [48][KP] (key blocks scaled for tiles (2,0), (3,0), (3,1)).
-  static constexpr int Lq = 0, Lk = Lq + 64 * KP, Rd = Lk + 64 * KP, Kap = Rd + 64 * KP, Far = Kap + 48 * KP;
-  static constexpr int U1_END = Far + 48 * KP;
-  // Region U2 overlays U1 in the column phase: Qt, Kh [64][KP]; KtT [K][TP].
-  static constexpr int Qt = 0, Kh = Qt + 64 * KP, KtT = Kh + 64 * KP;
-  static constexpr int U2_END = KtT + K * TP;
-  static_assert(U2_END <= U1_END, "column-phase operands must fit in the prep region");
-  static constexpr int Sc = U1_END;           // [64][TP] bf16 gated scores (lower block triangle)
-  static constexpr int NegL = Sc + 64 * TP;   // [64][TP] bf16 -L (off-diagonal blocks)
-  static constexpr int Ainv = NegL + 64 * TP; // [4][16][16] bf16 diagonal-block inverses
-  static constexpr int Vt = Ainv + 4 * 256;   // [64][TP] bf16 value tile of the slice
-  static constexpr int BF16_END = Vt + 64 * TP;
-  // fp32 regions (float offsets from the byte offset 2 * BF16_END, rounded up to 16 bytes)
-  static constexpr int F0 = ((2 * BF16_END + 15) / 16) * 4;
-  static constexpr int Lii = F0;                  // [4][16][17] fp32 strictly-lower diagonal blocks of L
-  static constexpr int Ostg = Lii + 4 * 16 * 17;  // [64][68] fp32 output staging
-  static constexpr int Beta = Ostg + 64 * 68;     // [64]
-  static constexpr int Tot = Beta + 64;           // [4][K] block totals of the log gate
-  static constexpr int Gam = Tot + 4 * K;         // [K] e^{b_end}
-  static constexpr int Hot = Gam + K;             // [4] per-block "has a hot channel" flags
-  static constexpr int F_END = Hot + 4;
-  static constexpr int BYTES = F_END * 4;
+  static constexpr int KP = K + 8;                // row pitch of [64][K] bf16 tiles (16-byte skew per row)
+  // consumer buffer, bf16 part (every decay factor folded into these operands is <= 1)
+  static constexpr int Lq = 0;                    // [64][KP] q e^{b - a_{blk-1}}   (block-start anchor)
+  static constexpr int Lk = Lq + 64 * KP;         // [64][KP] k e^{b - a_{blk-1}}
+  static constexpr int Kt = Lk + 64 * KP;         // [64][KP] k e^{b_end - b}       (chunk-end anchor)
+  static constexpr int Sc = Kt + 64 * KP;         // 10 tiles [16][16]: gated scores, tile (i, j<=i)
+  static constexpr int NegL = Sc + 10 * 256;      // 6 tiles [16][16]: -diag(beta) P, tile (i, j<i)
+  static constexpr int Ainv = NegL + 6 * 256;     // 4 tiles [16][16]: (I + diag(beta) P_ii)^{-1}
+  static constexpr int BF_END = Ainv + 4 * 256;
+  static constexpr int BETA = ((BF_END * 2 + 15) / 16) * 16;  // fp32 [64]
+  static constexpr int GAM = BETA + 64 * 4;                    // fp32 [K] e^{b_end}
+  static constexpr int ABLK = GAM + K * 4;                     // fp32 [3][K] e^{a_i}, i = 0..2 (block ends)
+  static constexpr int BUF = ABLK + 3 * K * 4;                 // bytes per consumer buffer
+  // producer-private region
+  static constexpr int KAP = 2 * BUF;             // bf16 [64][KP] k e^{a_blk - b}  (block-end anchor)
+  static constexpr int LII = KAP + 64 * KP * 2;   // fp32 [4][16][16] strictly-lower diagonal blocks of L
+  static constexpr int TOT = LII + 4 * 256 * 4;   // fp32 [2][4][K] per-block log-gate totals, by chunk parity
+  static constexpr int FAR = TOT + 2 * 4 * K * 4; // fp32 [3][K] key scalings of tiles (2,0), (3,0), (3,1)
+  static constexpr int RDS = FAR + 3 * K * 4;     // fp32 [4][K] e^{-T_blk} (0 for hot channels)
+  static constexpr int CNT = RDS + 4 * K * 4;     // int producer hand-off counter
+  static constexpr int BYTES = CNT + 16;
 };
+
+__device__ __forceinline__ int tri_tile(int i, int j) { return i * (i + 1) / 2 + j; }  // j <= i
+__device__ __forceinline__ int strict_tile(int i, int j) { return i * (i - 1) / 2 + j; }  // j < i
+
+// Transposing LDS read of four bf16 (ds_read_b64_tr_b16): within each 16-lane group, lane c slot r receives
+// element c % 4 of the 8 bytes addressed by lane 4 r + c / 4 of the group.
+__device__ __forceinline__ bf16x4 lds_read_tr(const unsigned char* smem, int byte_off) {
+  typedef short short4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) short4_t lds_short4;
+  const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_short4*)((__attribute__((address_space(3))) const unsigned char*)smem + byte_off));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+// Producers hand off to each other through an LDS counter; every producer wave arrives at every hand-off.
+__device__ __forceinline__ void producer_handoff(int* cnt, int target) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) __builtin_amdgcn_s_sleep(1);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Exact evaluation of the diagonal 16x16 block of the gated scores and kernel matrix for the channels of this
+// lane whose in-block decay span is too large for the block-start factorisation (bit c of hot_mask <-> channel
+// c0 + c).  Re-reads the block's q, k and gate rows (L2-resident), rebuilds the in-block cumulative gate and adds
+//   Sc(t, s) += sum_{hot c} q_tc k_sc e^{b_tc - b_sc}   (t >= s),   L(t, s) += beta_t sum_{hot c} k_tc k_sc e^{...}  (t > s)
+// to the tiles the MFMA pass produced with zero key operands for those channels.
+template <int K, bool kDelta, int kGate>
+__device__ __forceinline__ void hot_diag_fixup(const __bf16* qp, const __bf16* kp, const float* gp, int64_t q_st,
+                                            int64_t k_st, int64_t g_st, int chunk_row0, int len, int pw,
+                                            uint32_t hot_mask, __bf16* sc_tile, float* lii_tile,
+                                            const float* beta_rows) {
+  constexpr int LPR = K / 8, RSG = kWave / LPR, RPL = 16 / RSG;
+  const int lane = threadIdx.x & 63;
+  const int cg = lane % LPR, rs = lane / LPR, c0 = 8 * cg;
+  uint4 hq[RPL], hk[RPL];
+  float hb[RPL][8];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    const int t = chunk_row0 + 16 * pw + rs * RPL + j;
+    const bool ok = t < len;
+    hq[j] = ok ? *reinterpret_cast<const uint4*>(qp + t * q_st + c0) : make_uint4(0, 0, 0, 0);
+    hk[j] = ok ? *reinterpret_cast<const uint4*>(kp + t * k_st + c0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) hb[j][c] = ok ? (kGate == 2 ? gp[t * g_st + c0 + c] : gp[t * g_st]) : 0.f;
+  }
+#pragma unroll
+  for (int j = 1; j < RPL; ++j)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) hb[j][c] += hb[j - 1][c];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const float own = hb[RPL - 1][c];
+    float incl = own;
+#pragma unroll
+    for (int off = LPR; off < kWave; off *= 2) {
+      const float y = __shfl_up(incl, off, kWave);
+      if (lane >= off) incl += y;
+    }
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) hb[j][c] += incl - own;
+  }
+#pragma unroll 1
+  for (int sr = 0; sr < 16; ++sr) {
+    const int src = cg + LPR * (sr / RPL);
+    const int js = sr % RPL;
+    float pa[RPL], sa[RPL];
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) pa[j] = sa[j] = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float kv = 0.f, bv = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < RPL; ++jj) {
+        if (jj == js) {
+          kv = bf16_elem(hk[jj], c);
+          bv = hb[jj][c];
+        }
+      }
+      const float ks = __shfl(kv, src, kWave), bs = __shfl(bv, src, kWave);
+      if (hot_mask & (1u << c)) {
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) {
+          const float d = ks * exp_fast(fminf(hb[j][c] - bs, 0.f));
+          pa[j] += bf16_elem(hk[j], c) * d;
+          sa[j] += bf16_elem(hq[j], c) * d;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) {
+#pragma unroll
+      for (int m = 1; m < LPR; m *= 2) {
+        pa[j] += shfl_xor(pa[j], m);
+        sa[j] += shfl_xor(sa[j], m);
+      }
+      const int t = rs * RPL + j;
+      if (cg == 0 && t >= sr) {
+        __bf16* dst = sc_tile + t * 16 + sr;
+        *dst = bf(f32(*dst) + sa[j]);
+        if (kDelta && t > sr) lii_tile[t * 16 + sr] += beta_rows[t] * pa[j];
+      }
+    }
+  }
+}
 
 }  // namespace
 
 template <int VARIANT, int K, typename OutT>
-__global__ __launch_bounds__(256, 1) void chunk_fwd_kernel(const gdr_args a, int n_slices, int xcd_map) {
+__global__ __launch_bounds__(512, 1) void chunk_fwd_kernel(const gdr_args a, int n_slices, int xcd_map) {
   constexpr bool kDelta = VARIANT != GDR_GLA;
   constexpr int kGate = (VARIANT == GDR_KDA || VARIANT == GDR_GLA) ? 2 : (VARIANT == GDR_GDN ? 1 : 0);
-  constexpr int LPR = K / 8;       // prep lanes per row (8 channels each)
-  constexpr int RSG = kWave / LPR; // row subgroups per wave
-  constexpr int RPL = 16 / RSG;    // rows per prep lane
+  constexpr int LPR = K / 8;       // producer lanes per row (8 channels each)
+  constexpr int RSG = kWave / LPR; // row subgroups per producer wave
+  constexpr int RPL = 16 / RSG;    // rows per producer lane
   constexpr int KT = K / 16;       // 16-channel tiles of the state
   constexpr int KS = K / 32;       // k-steps of 32 channels
   using M = Lds<K>;
-  constexpr int KP = M::KP, TP = M::TP;
+  constexpr int KP = M::KP;
 
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  __bf16* sb = reinterpret_cast<__bf16*>(smem_raw);
-  float* sf = reinterpret_cast<float*>(smem_raw);
+  extern __shared__ __align__(16) unsigned char smem[];
 
   // ---- workgroup -> (sequence, head, value slice); XCD-aware so the slices of one head share an L2 ----
   const int x = blockIdx.x;
@@ -172,404 +279,429 @@ __global__ __launch_bounds__(256, 1) void chunk_fwd_kernel(const gdr_args a, int
     len = hi - lo;
     bidx = 0;
   }
+  const int nchunks = (len + kChunk - 1) / kChunk;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
-  const int v0 = slice * kSlice;
-  const int col = v0 + 16 * wave + l16;  // this lane's state/output column in the column phase
+  const bool producer = wave >= 4;
+  int* cnt = reinterpret_cast<int*>(smem + M::CNT);
+  if (tid == 0) *cnt = 0;
 
-  const __bf16* qp = static_cast<const __bf16*>(a.q.ptr) + bidx * a.q.stride_b + h * a.q.stride_h +
-                     int64_t(bos) * a.q.stride_t;
-  const __bf16* kp = static_cast<const __bf16*>(a.k.ptr) + bidx * a.k.stride_b + h * a.k.stride_h +
-                     int64_t(bos) * a.k.stride_t;
-  const __bf16* vp = static_cast<const __bf16*>(a.v.ptr) + bidx * a.v.stride_b + h * a.v.stride_h +
-                     int64_t(bos) * a.v.stride_t;
+  const int64_t q_st = a.q.stride_t, k_st = a.k.stride_t, v_st = a.v.stride_t, o_st = a.out.stride_t;
+  const int64_t g_st = a.gate.stride_t, b_st = a.beta.stride_t;
+  const __bf16* qp = static_cast<const __bf16*>(a.q.ptr) + bidx * a.q.stride_b + h * a.q.stride_h + bos * q_st;
+  const __bf16* kp = static_cast<const __bf16*>(a.k.ptr) + bidx * a.k.stride_b + h * a.k.stride_h + bos * k_st;
+  const __bf16* vp = static_cast<const __bf16*>(a.v.ptr) + bidx * a.v.stride_b + h * a.v.stride_h + bos * v_st;
   const float* gp = kGate ? static_cast<const float*>(a.gate.ptr) + bidx * a.gate.stride_b +
-                                h * a.gate.stride_h + int64_t(bos) * a.gate.stride_t
+                                h * a.gate.stride_h + bos * g_st
                           : nullptr;
   const float* betap = kDelta ? static_cast<const float*>(a.beta.ptr) + bidx * a.beta.stride_b +
-                                    h * a.beta.stride_h + int64_t(bos) * a.beta.stride_t
+                                    h * a.beta.stride_h + bos * b_st
                               : nullptr;
   OutT* op = static_cast<OutT*>(const_cast<void*>(a.out.ptr)) + bidx * a.out.stride_b + h * a.out.stride_h +
-             int64_t(bos) * a.out.stride_t;
+             bos * o_st;
   const size_t sbase = size_t(n * H + h) * K * V;
+  const int v0 = slice * kSlice;
 
-  // ---- state slice in accumulator layout: st[m][i] = S[16 m + 4 g4 + i][col] ----
-  floatx4 st[KT];
-#pragma unroll
-  for (int m = 0; m < KT; ++m)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) st[m][i] = a.h0 ? a.h0[sbase + size_t(16 * m + 4 * g4 + i) * V + col] : 0.f;
+  if (producer) {
+    // =============================== producers: waves 4..7, wave p <-> block p ===============================
+    const int pw = wave - 4;
+    const int cg = lane % LPR, rs = lane / LPR, c0 = 8 * cg;
+    const int row0 = 16 * pw + rs * RPL;  // chunk-local row of this lane's first element
+    __bf16* kap = reinterpret_cast<__bf16*>(smem + M::KAP);
+    float* lii = reinterpret_cast<float*>(smem + M::LII) + pw * 256;
+    float* tot = reinterpret_cast<float*>(smem + M::TOT);
+    float* far = reinterpret_cast<float*>(smem + M::FAR);
 
-  // prep-lane geometry: lane holds rows 16 wave + rs * RPL + j (j < RPL), channels c0 .. c0 + 7
-  const int cg = lane % LPR, rs = lane / LPR, c0 = 8 * cg;
-  const float scale = a.scale;
-  const int nchunks = (len + kChunk - 1) / kChunk;
-
-  for (int ci = 0; ci < nchunks; ++ci) {
-    const int t0 = ci * kChunk;
-    // =========================== step a: loads and in-block gate prefix ===========================
-    float qf[RPL][8], kf[RPL][8], bl[RPL][8];
+    // raw inputs of one chunk for this lane: q, k rows (8 bf16 each), gate (8 fp32 or one scalar), beta
+    uint4 cq[RPL], ck[RPL];
+    float bl[RPL][8], ng[RPL][8], cb[RPL];
+    // Loads are unconditional from clamped rows (len >= 1 whenever a chunk exists) and masked afterwards, so the
+    // compiler never has to wait on a load inside a branch.
+    auto load_qk = [&](int chunk, uint4* rq, uint4* rk, float* rb) {
 #pragma unroll
-    for (int j = 0; j < RPL; ++j) {
-      const int t = t0 + 16 * wave + rs * RPL + j;
-      if (t < len) {
-        unpack8(*reinterpret_cast<const uint4*>(qp + t * a.q.stride_t + c0), qf[j]);
-        unpack8(*reinterpret_cast<const uint4*>(kp + t * a.k.stride_t + c0), kf[j]);
+      for (int j = 0; j < RPL; ++j) {
+        const int t = chunk * kChunk + row0 + j;
+        const int tc = min(t, len - 1);
+        const uint32_t keep = t < len ? 0xffffffffu : 0u;
+        const uint4 qv = *reinterpret_cast<const uint4*>(qp + tc * q_st + c0);
+        const uint4 kv = *reinterpret_cast<const uint4*>(kp + tc * k_st + c0);
+        rq[j] = make_uint4(qv.x & keep, qv.y & keep, qv.z & keep, qv.w & keep);
+        rk[j] = make_uint4(kv.x & keep, kv.y & keep, kv.z & keep, kv.w & keep);
+        if constexpr (kDelta) {
+          const float bv = betap[tc * b_st];
+          rb[j] = t < len ? bv : 0.f;
+        }
+      }
+    };
+    auto load_g = [&](int chunk, float (*rg)[8]) {
+#pragma unroll
+      for (int j = 0; j < RPL; ++j) {
+        const int t = chunk * kChunk + row0 + j;
+        const int tc = min(t, len - 1);
+        const bool ok = t < len;
         if constexpr (kGate == 2) {
-          const float4 g0 = *reinterpret_cast<const float4*>(gp + t * a.gate.stride_t + c0);
-          const float4 g1 = *reinterpret_cast<const float4*>(gp + t * a.gate.stride_t + c0 + 4);
-          bl[j][0] = g0.x; bl[j][1] = g0.y; bl[j][2] = g0.z; bl[j][3] = g0.w;
-          bl[j][4] = g1.x; bl[j][5] = g1.y; bl[j][6] = g1.z; bl[j][7] = g1.w;
+          const float4 g0 = *reinterpret_cast<const float4*>(gp + tc * g_st + c0);
+          const float4 g1 = *reinterpret_cast<const float4*>(gp + tc * g_st + c0 + 4);
+          rg[j][0] = ok ? g0.x : 0.f; rg[j][1] = ok ? g0.y : 0.f; rg[j][2] = ok ? g0.z : 0.f;
+          rg[j][3] = ok ? g0.w : 0.f; rg[j][4] = ok ? g1.x : 0.f; rg[j][5] = ok ? g1.y : 0.f;
+          rg[j][6] = ok ? g1.z : 0.f; rg[j][7] = ok ? g1.w : 0.f;
         } else if constexpr (kGate == 1) {
-          const float g = gp[t * a.gate.stride_t];
+          const float g = gp[tc * g_st];
 #pragma unroll
-          for (int c = 0; c < 8; ++c) bl[j][c] = g;
+          for (int c = 0; c < 8; ++c) rg[j][c] = ok ? g : 0.f;
         } else {
 #pragma unroll
-          for (int c = 0; c < 8; ++c) bl[j][c] = 0.f;
+          for (int c = 0; c < 8; ++c) rg[j][c] = 0.f;
         }
-      } else {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) qf[j][c] = kf[j][c] = bl[j][c] = 0.f;
       }
-    }
-    if constexpr (kGate) {
+    };
+    // in-block inclusive prefix of the log gate; block totals to tot[slot]
+    auto scan = [&](float (*g)[8], int slot, bool write_tot) {
+      if constexpr (kGate) {
 #pragma unroll
-      for (int j = 1; j < RPL; ++j)
+        for (int j = 1; j < RPL; ++j)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) bl[j][c] += bl[j - 1][c];
-      // inclusive scan of the lane totals over the RSG lanes that share this channel group
+          for (int c = 0; c < 8; ++c) g[j][c] += g[j - 1][c];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const float tot = bl[RPL - 1][c];
-        float incl = tot;
+        for (int c = 0; c < 8; ++c) {
+          const float own = g[RPL - 1][c];
+          float incl = own;
 #pragma unroll
-        for (int off = LPR; off < kWave; off *= 2) {
-          const float y = __shfl_up(incl, off, kWave);
-          if (lane >= off) incl += y;
+          for (int off = LPR; off < kWave; off *= 2) {
+            const float y = __shfl_up(incl, off, kWave);
+            if (lane >= off) incl += y;
+          }
+          const float excl = incl - own;
+#pragma unroll
+          for (int j = 0; j < RPL; ++j) g[j][c] += excl;
         }
-        const float excl = incl - tot;
+        if (write_tot && rs == RSG - 1) {
 #pragma unroll
-        for (int j = 0; j < RPL; ++j) bl[j][c] += excl;
+          for (int c = 0; c < 8; ++c) tot[(slot * 4 + pw) * K + c0 + c] = g[RPL - 1][c];
+        }
       }
-      if (rs == RSG - 1) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) sf[M::Tot + wave * K + c0 + c] = bl[RPL - 1][c];
-      }
-    }
-    // value tile of the slice and beta
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int chunk16 = tid + 256 * r;  // 512 pieces of 8 bf16
-      const int row = chunk16 >> 3, cc = (chunk16 & 7) * 8;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (t0 + row < len) val = *reinterpret_cast<const uint4*>(vp + (t0 + row) * a.v.stride_t + v0 + cc);
-      *reinterpret_cast<uint4*>(sb + M::Vt + row * TP + cc) = val;
-    }
-    if (tid < kChunk) {
-      float bv = 0.f;
-      if constexpr (kDelta) {
-        if (t0 + tid < len) bv = betap[(t0 + tid) * a.beta.stride_t];
-      }
-      sf[M::Beta + tid] = bv;
+    };
+
+    // prologue: chunk 0 loaded and scanned
+    if (nchunks > 0) {
+      load_qk(0, cq, ck, cb);
+      load_g(0, bl);
+      scan(bl, 0, true);
     }
     __syncthreads();
 
-    // =========================== step b: decay factors and prep-phase operands ===========================
-    float ea_prev[8], eb_tail[8], tw[8], far1[8], far2[8];
-    bool hot[8];
-    bool any_hot = false;
+    for (int s = 0; s <= nchunks; ++s) {
+      if (s < nchunks) {
+        const int slot = s & 1;
+        __bf16* buf = reinterpret_cast<__bf16*>(smem + slot * M::BUF);
+        float* bbeta = reinterpret_cast<float*>(smem + slot * M::BUF + M::BETA);
+        float* bgam = reinterpret_cast<float*>(smem + slot * M::BUF + M::GAM);
+
+        // ---- decay factors and operands of chunk s ----
+        float* ablk = reinterpret_cast<float*>(smem + slot * M::BUF + M::ABLK);
+        float* rds = reinterpret_cast<float*>(smem + M::RDS);
+        float eb[8], tw[8];
+        bool hot[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      ea_prev[c] = eb_tail[c] = far1[c] = far2[c] = 1.f;
-      tw[c] = 0.f;
-      hot[c] = false;
-    }
-    if constexpr (kGate) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        float tb[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) tb[m] = sf[M::Tot + m * K + c0 + c];
-        float prev = 0.f, tail = 0.f;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          if (m < wave) prev += tb[m];
-          if (m > wave) tail += tb[m];
+        for (int c = 0; c < 8; ++c) {
+          eb[c] = 1.f;
+          tw[c] = 0.f;
+          hot[c] = false;
         }
-        tw[c] = tb[wave];
-        ea_prev[c] = exp_fast(prev);
-        eb_tail[c] = exp_fast(tail);
-        hot[c] = -tw[c] > kHotSpan;
-        any_hot |= hot[c];
-        // far-tile scalings: wave 0 -> tiles (2,0) e^{T1} and (3,0) e^{T1+T2}; wave 1 -> tile (3,1) e^{T2}
-        far1[c] = exp_fast(wave == 0 ? tb[1] : tb[2]);
-        far2[c] = exp_fast(tb[1] + tb[2]);
-        if (wave == 0 && rs == 0) sf[M::Gam + c0 + c] = exp_fast(tb[0] + tb[1] + tb[2] + tb[3]);
-      }
-    } else {
-      if (wave == 0 && rs == 0) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) sf[M::Gam + c0 + c] = 1.f;
-      }
-    }
-    float ell[RPL][8], rho[RPL][8];
-#pragma unroll
-    for (int j = 0; j < RPL; ++j) {
-      const int tl = 16 * wave + rs * RPL + j;  // chunk-local row
-      float rd[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
         if constexpr (kGate) {
-          ell[j][c] = exp_fast(bl[j][c]);
-          rho[j][c] = exp_fast(tw[c] - bl[j][c]);
-          rd[c] = hot[c] ? 0.f : kf[j][c] * exp_fast(-bl[j][c]);
-        } else {
-          ell[j][c] = rho[j][c] = 1.f;
-          rd[c] = kf[j][c];
-        }
-      }
-      float lq[8], lk[8], kap[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        lq[c] = qf[j][c] * ell[j][c];
-        lk[c] = kf[j][c] * ell[j][c];
-        kap[c] = kf[j][c] * rho[j][c];
-      }
-      store8(sb + M::Lq + tl * KP + c0, lq, scale);
-      store8(sb + M::Lk + tl * KP + c0, lk, 1.f);
-      store8(sb + M::Rd + tl * KP + c0, rd, 1.f);
-      if (wave < 3) store8(sb + M::Kap + tl * KP + c0, kap, 1.f);
-      if (wave < 2) {
-        float f1[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) f1[c] = kap[c] * far1[c];
-        // Far rows: [0,16) tile (2,0), [16,32) tile (3,0), [32,48) tile (3,1)
-        if (wave == 0) {
-          float f2[8];
-#pragma unroll
-          for (int c = 0; c < 8; ++c) f2[c] = kap[c] * far2[c];
-          store8(sb + M::Far + tl * KP + c0, f1, 1.f);
-          store8(sb + M::Far + (16 + tl) * KP + c0, f2, 1.f);
-        } else {
-          store8(sb + M::Far + (32 + tl - 16) * KP + c0, f1, 1.f);
-        }
-      }
-    }
-    if constexpr (kGate) {
-      const bool wave_hot = __any(any_hot);
-      if (lane == 0) sf[M::Hot + wave] = wave_hot ? 1.f : 0.f;
-    }
-    __syncthreads();
-
-    // =========================== step c: gated score / kernel-matrix strips (wave w: query block w) ============
-    for (int j = 0; j <= wave; ++j) {
-      int key_off;
-      if (j == wave) key_off = M::Rd + 16 * j * KP;
-      else if (j == wave - 1) key_off = M::Kap + 16 * j * KP;
-      else if (wave == 2) key_off = M::Far;             // (2,0)
-      else if (j == 0) key_off = M::Far + 16 * KP;      // (3,0)
-      else key_off = M::Far + 32 * KP;                  // (3,1)
-      floatx4 acc_s = {0.f, 0.f, 0.f, 0.f}, acc_p = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        const int kc = 32 * kk + 8 * g4;
-        const bf16x8 bk = *reinterpret_cast<const bf16x8*>(sb + key_off + l16 * KP + kc);
-        const bf16x8 aq = *reinterpret_cast<const bf16x8*>(sb + M::Lq + (16 * wave + l16) * KP + kc);
-        acc_s = mfma32(aq, bk, acc_s);
-        if constexpr (kDelta) {
-          const bf16x8 ak = *reinterpret_cast<const bf16x8*>(sb + M::Lk + (16 * wave + l16) * KP + kc);
-          acc_p = mfma32(ak, bk, acc_p);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tloc = 4 * g4 + i, sloc = l16;
-        const int row = 16 * wave + tloc;
-        float s = acc_s[i];
-        if (j == wave && tloc < sloc) s = 0.f;
-        sb[M::Sc + row * TP + 16 * j + sloc] = bf(s);
-        if constexpr (kDelta) {
-          const float p = acc_p[i] * sf[M::Beta + row];
-          if (j < wave) sb[M::NegL + row * TP + 16 * j + sloc] = bf(-p);
-          else sf[M::Lii + wave * 272 + tloc * 17 + sloc] = tloc > sloc ? p : 0.f;
-        }
-      }
-    }
-    __syncthreads();
-
-    // exact elementwise diagonal blocks for channels whose in-block decay span is too large for a factorisation
-    if constexpr (kGate) {
-      if (sf[M::Hot + wave] != 0.f) {
-        for (int s = 0; s < 16; ++s) {
-          const int src = cg + LPR * (s / RPL);
-          const int js = s % RPL;
-          float ks[8], bs[8];
 #pragma unroll
           for (int c = 0; c < 8; ++c) {
-            float kv = 0.f, bv = 0.f;
+            float tb[4];
 #pragma unroll
-            for (int jj = 0; jj < RPL; ++jj) {
-              if (jj == js) {
-                kv = kf[jj][c];
-                bv = bl[jj][c];
+            for (int m = 0; m < 4; ++m) tb[m] = tot[(slot * 4 + m) * K + c0 + c];
+            float tail = 0.f;
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+              if (m > pw) tail += tb[m];
+            tw[c] = tb[pw];
+            eb[c] = exp_fast(tail);
+            hot[c] = -tw[c] > kHotSpan;
+            if (rs == 0) {
+              rds[pw * K + c0 + c] = hot[c] ? 0.f : exp_fast(-tw[c]);
+              if (pw < 3) {
+                float upto = 0.f;
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                  if (m <= pw) upto += tb[m];
+                ablk[pw * K + c0 + c] = exp_fast(upto);
+              }
+              if (pw == 0) {
+                bgam[c0 + c] = exp_fast(tb[0] + tb[1] + tb[2] + tb[3]);
+                far[0 * K + c0 + c] = exp_fast(tb[1]);          // tile (2,0)
+                far[1 * K + c0 + c] = exp_fast(tb[1] + tb[2]);  // tile (3,0)
+                far[2 * K + c0 + c] = exp_fast(tb[2]);          // tile (3,1)
               }
             }
-            ks[c] = __shfl(kv, src, kWave);
-            bs[c] = __shfl(bv, src, kWave);
+          }
+        } else if (rs == 0) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            rds[pw * K + c0 + c] = 1.f;
+            if (pw < 3) ablk[pw * K + c0 + c] = 1.f;
+            if (pw == 0) {
+              bgam[c0 + c] = 1.f;
+              far[0 * K + c0 + c] = far[1 * K + c0 + c] = far[2 * K + c0 + c] = 1.f;
+            }
+          }
+        }
+        if constexpr (kDelta) {
+          if (cg == 0) {
+#pragma unroll
+            for (int j = 0; j < RPL; ++j) bbeta[row0 + j] = cb[j];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) {
+          const int row = row0 + j;
+          float qf[8], kf[8];
+          unpack8(cq[j], qf);
+          unpack8(ck[j], kf);
+          bf16x8 lq, lk, kv, kt;
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            float ell = 1.f, rho = 1.f;
+            if constexpr (kGate) {
+              ell = exp_fast(bl[j][c]);
+              rho = exp_fast(tw[c] - bl[j][c]);
+            }
+            const float kapf = kf[c] * rho;
+            lq[c] = bf(qf[c] * ell);
+            lk[c] = bf(kf[c] * ell);
+            kv[c] = bf(kapf);
+            kt[c] = bf(kapf * eb[c]);
+          }
+          *reinterpret_cast<bf16x8*>(buf + M::Lq + row * KP + c0) = lq;
+          *reinterpret_cast<bf16x8*>(buf + M::Lk + row * KP + c0) = lk;
+          *reinterpret_cast<bf16x8*>(buf + M::Kt + row * KP + c0) = kt;
+          *reinterpret_cast<bf16x8*>(kap + row * KP + c0) = kv;
+        }
+        producer_handoff(cnt, 4 * (s + 1));
+        if (s + 1 < nchunks) load_g(s + 1, ng);
+
+        // ---- gated strips of query block pw: Sc(pw, j) and P(pw, j) for j <= pw ----
+        for (int j = 0; j <= pw; ++j) {
+          // key operand of tile (pw, j): k e^{a_{pw-1} - b} = Kap_j scaled by e^{a_{pw-1} - a_j} (<= 1) or,
+          // on the diagonal, by e^{-T_pw} (>= 1, bounded by the block span; 0 for hot channels)
+          const float* kscale = (j == pw) ? rds + pw * K : far + ((pw == 2) ? 0 : (j == 0 ? 1 : 2)) * K;
+          const bool scaled = (j == pw) || (j + 2 <= pw);
+          floatx4 acc_s = {0.f, 0.f, 0.f, 0.f}, acc_p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kk = 0; kk < KS; ++kk) {
+            const int kc = 32 * kk + 8 * g4;
+            bf16x8 bk = *reinterpret_cast<const bf16x8*>(kap + (16 * j + l16) * KP + kc);
+            if (scaled) {
+              const float4 f0 = *reinterpret_cast<const float4*>(kscale + kc);
+              const float4 f1 = *reinterpret_cast<const float4*>(kscale + kc + 4);
+              const float f[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+              for (int c = 0; c < 8; ++c) bk[c] = bf(f32(bk[c]) * f[c]);
+            }
+            const bf16x8 aq = *reinterpret_cast<const bf16x8*>(buf + M::Lq + (16 * pw + l16) * KP + kc);
+            acc_s = mfma32(aq, bk, acc_s);
+            if constexpr (kDelta) {
+              const bf16x8 ak = *reinterpret_cast<const bf16x8*>(buf + M::Lk + (16 * pw + l16) * KP + kc);
+              acc_p = mfma32(ak, bk, acc_p);
+            }
           }
 #pragma unroll
-          for (int j = 0; j < RPL; ++j) {
-            const int t = rs * RPL + j;
-            float p = 0.f, sc = 0.f;
+          for (int r = 0; r < 4; ++r) {
+            const int tloc = 4 * g4 + r, sloc = l16;
+            float sv = acc_s[r];
+            if (j == pw && tloc < sloc) sv = 0.f;
+            buf[M::Sc + tri_tile(pw, j) * 256 + tloc * 16 + sloc] = bf(sv);
+            if constexpr (kDelta) {
+              const float p = acc_p[r] * bbeta[16 * pw + tloc];
+              if (j < pw) buf[M::NegL + strict_tile(pw, j) * 256 + tloc * 16 + sloc] = bf(-p);
+              else lii[tloc * 16 + sloc] = tloc > sloc ? p : 0.f;
+            }
+          }
+        }
+        // exact elementwise diagonal block for hot channels (rare; out of line to keep the common path's
+        // registers free)
+        if constexpr (kGate) {
+          uint32_t hot_mask = 0;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-              if (hot[c]) {
-                const float d = exp_fast(fminf(bl[j][c] - bs[c], 0.f));
-                p += kf[j][c] * ks[c] * d;
-                sc += qf[j][c] * ks[c] * d;
+          for (int c = 0; c < 8; ++c) hot_mask |= hot[c] ? (1u << c) : 0u;
+          if (__any(hot_mask != 0)) {
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            hot_diag_fixup<K, kDelta, kGate>(qp, kp, gp, q_st, k_st, g_st, s * kChunk, len, pw, hot_mask,
+                                             buf + M::Sc + tri_tile(pw, pw) * 256, lii, bbeta + 16 * pw);
+          }
+        }
+        if constexpr (kDelta) {
+          __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+          if (lane < 16) {  // column `lane` of (I + L_pp)^{-1} by forward substitution in fp32
+            float xcol[16];
+            xcol[0] = lane == 0 ? 1.f : 0.f;
+#pragma unroll
+            for (int r = 1; r < 16; ++r) {
+              float lrow[16];
+#pragma unroll
+              for (int m4 = 0; m4 < (r + 3) / 4; ++m4) {
+                const float4 v = *reinterpret_cast<const float4*>(lii + r * 16 + 4 * m4);
+                lrow[4 * m4] = v.x; lrow[4 * m4 + 1] = v.y; lrow[4 * m4 + 2] = v.z; lrow[4 * m4 + 3] = v.w;
               }
+              float acc0 = (r == lane) ? 1.f : 0.f, acc1 = 0.f;
+#pragma unroll
+              for (int m = 0; m < r; m += 2) {
+                acc0 -= lrow[m] * xcol[m];
+                if (m + 1 < r) acc1 -= lrow[m + 1] * xcol[m + 1];
+              }
+              xcol[r] = acc0 + acc1;
             }
 #pragma unroll
-            for (int m = 1; m < LPR; m *= 2) {
-              p += shfl_xor(p, m);
-              sc += shfl_xor(sc, m);
-            }
-            if (cg == 0 && t >= s) {
-              const int row = 16 * wave + t;
-              __bf16* dst = sb + M::Sc + row * TP + 16 * wave + s;
-              *dst = bf(f32(*dst) + scale * sc);
-              if (kDelta && t > s) sf[M::Lii + wave * 272 + t * 17 + s] += sf[M::Beta + row] * p;
-            }
+            for (int r = 0; r < 16; ++r) buf[M::Ainv + pw * 256 + r * 16 + lane] = bf(xcol[r]);
           }
         }
-      }
-    }
-    __syncthreads();
-
-    // =========================== step d: column-phase operands (overlay U1) and diagonal inverses ===========
+        // ---- chunk s + 1 becomes current ----
+        if (s + 1 < nchunks) {
 #pragma unroll
-    for (int j = 0; j < RPL; ++j) {
-      const int tl = 16 * wave + rs * RPL + j;
-      float qt[8], kh[8];
+          for (int j = 0; j < RPL; ++j)
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        qt[c] = qf[j][c] * ell[j][c] * ea_prev[c];
-        kh[c] = kf[j][c] * ell[j][c] * ea_prev[c];
-      }
-      store8(sb + M::Qt + tl * KP + c0, qt, scale);
-      store8(sb + M::Kh + tl * KP + c0, kh, 1.f);
-    }
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int tl0 = 16 * wave + rs * RPL;
-#pragma unroll
-      for (int j = 0; j < RPL; ++j)
-        sb[M::KtT + (c0 + c) * TP + tl0 + j] = bf(kf[j][c] * rho[j][c] * eb_tail[c]);
-    }
-    if constexpr (kDelta) {
-      if (lane < 16) {  // column `lane` of (I + L_ww)^{-1}, forward substitution in fp32
-        const float* Lw = sf + M::Lii + wave * 272;
-        float xcol[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float acc = (r == lane) ? 1.f : 0.f;
-#pragma unroll
-          for (int m = 0; m < r; ++m) acc -= Lw[r * 17 + m] * xcol[m];
-          xcol[r] = acc;
+            for (int c = 0; c < 8; ++c) bl[j][c] = ng[j][c];
+          scan(bl, (s + 1) & 1, true);
+          load_qk(s + 1, cq, ck, cb);  // lands while the next step's decay factors are formed
         }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sb[M::Ainv + wave * 256 + r * 16 + lane] = bf(xcol[r]);
       }
+      __syncthreads();
     }
-    __syncthreads();
-
-    // =========================== step e: column work (wave w: 16 value columns) ===========================
-    bf16x8 sB[KS];
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) sB[kk] = concat(pack4(st[2 * kk]), pack4(st[2 * kk + 1]));
-    floatx4 acc_o[4], yv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      floatx4 ax = {0.f, 0.f, 0.f, 0.f}, ao = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        const int r0 = (16 * i + l16) * KP + 32 * kk + 4 * g4;
-        const bf16x8 ak = concat(*reinterpret_cast<const bf16x4*>(sb + M::Kh + r0),
-                                 *reinterpret_cast<const bf16x4*>(sb + M::Kh + r0 + 16));
-        const bf16x8 aq = concat(*reinterpret_cast<const bf16x4*>(sb + M::Qt + r0),
-                                 *reinterpret_cast<const bf16x4*>(sb + M::Qt + r0 + 16));
-        if constexpr (kDelta) ax = mfma32(ak, sB[kk], ax);
-        ao = mfma32(aq, sB[kk], ao);
-      }
-      acc_o[i] = ao;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int row = 16 * i + 4 * g4 + jj;
-        const float vv = f32(sb[M::Vt + row * TP + 16 * wave + l16]);
-        yv[i][jj] = kDelta ? sf[M::Beta + row] * (vv - ax[jj]) : vv;
-      }
-    }
-    bf16x4 ub[4];
-    if constexpr (kDelta) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        floatx4 z = yv[i];
-#pragma unroll
-        for (int j = 0; j < i; ++j) {
-          const bf16x4 nl =
-              *reinterpret_cast<const bf16x4*>(sb + M::NegL + (16 * i + l16) * TP + 16 * j + 4 * g4);
-          z = mfma16(nl, ub[j], z);
-        }
-        const bf16x4 ai = *reinterpret_cast<const bf16x4*>(sb + M::Ainv + i * 256 + l16 * 16 + 4 * g4);
-        const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
-        ub[i] = pack4(mfma16(ai, pack4(z), zero));
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ub[i] = pack4(yv[i]);
-    }
-    // intra-chunk output
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j <= i; ++j) {
-        const bf16x4 sc = *reinterpret_cast<const bf16x4*>(sb + M::Sc + (16 * i + l16) * TP + 16 * j + 4 * g4);
-        acc_o[i] = mfma16(sc, ub[j], acc_o[i]);
-      }
-    }
-    // state update  S = diag(gamma) S + Kt^T u
-#pragma unroll
-    for (int m = 0; m < KT; ++m) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st[m][i] *= sf[M::Gam + 16 * m + 4 * g4 + i];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const int r0 = (16 * m + l16) * TP + 32 * kk + 4 * g4;
-        const bf16x8 ak = concat(*reinterpret_cast<const bf16x4*>(sb + M::KtT + r0),
-                                 *reinterpret_cast<const bf16x4*>(sb + M::KtT + r0 + 16));
-        st[m] = mfma32(ak, concat(ub[2 * kk], ub[2 * kk + 1]), st[m]);
-      }
-    }
-    // stage the output tile, then write full rows
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) sf[M::Ostg + (16 * i + 4 * g4 + jj) * 68 + 16 * wave + l16] = acc_o[i][jj];
-    __syncthreads();
-    {
-      const int row = tid >> 2, cc = (tid & 3) * 16;
-      if (t0 + row < len) store_row16<OutT>(op + (t0 + row) * a.out.stride_t + v0 + cc, sf + M::Ostg + row * 68 + cc);
-    }
-    __syncthreads();
-  }
-
-  if (a.ht) {
+  } else {
+    // =============================== consumers: waves 0..3, 16 state columns each ===============================
+    const int cw = wave;
+    const int col = v0 + 16 * cw + l16;
+    floatx4 st[KT];
 #pragma unroll
     for (int m = 0; m < KT; ++m)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a.ht[sbase + size_t(16 * m + 4 * g4 + i) * V + col] = st[m][i];
+      for (int r = 0; r < 4; ++r) st[m][r] = a.h0 ? a.h0[sbase + size_t(16 * m + 4 * g4 + r) * V + col] : 0.f;
+    // value tile of the next chunk in accumulator layout (row 16 i + 4 g4 + r), loaded unconditionally from
+    // clamped rows; rows past the end are zeroed when consumed
+    uint16_t vn[4][4];
+    auto load_v = [&](int chunk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = min(chunk * kChunk + 16 * i + 4 * g4 + r, len - 1);
+          vn[i][r] = reinterpret_cast<const uint16_t*>(vp)[t * v_st + col];
+        }
+    };
+    if (nchunks > 0) load_v(0);
+    __syncthreads();
+
+    const float scale = a.scale;
+    for (int s = 0; s <= nchunks; ++s) {
+      if (s >= 1) {
+        const int c = s - 1, slot = c & 1;
+        const __bf16* buf = reinterpret_cast<const __bf16*>(smem + slot * M::BUF);
+        const float* bbeta = reinterpret_cast<const float*>(smem + slot * M::BUF + M::BETA);
+        const float* bgam = reinterpret_cast<const float*>(smem + slot * M::BUF + M::GAM);
+        float vc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            vc[i][r] = (c * kChunk + 16 * i + 4 * g4 + r < len) ? bf16_bits_to_f32(vn[i][r]) : 0.f;
+        if (c + 1 < nchunks) load_v(c + 1);
+
+        const float* ablk = reinterpret_cast<const float*>(smem + slot * M::BUF + M::ABLK);
+        floatx4 acc_o[4], yv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // state operand of query block i: diag(e^{a_{i-1}}) S in bf16 (block-start anchor of Lq/Lk)
+          bf16x8 sB[KS];
+#pragma unroll
+          for (int kk = 0; kk < KS; ++kk) {
+            floatx4 lo = st[2 * kk], hi = st[2 * kk + 1];
+            if (i > 0) {
+              const float4 f0 = *reinterpret_cast<const float4*>(ablk + (i - 1) * K + 32 * kk + 4 * g4);
+              const float4 f1 = *reinterpret_cast<const float4*>(ablk + (i - 1) * K + 32 * kk + 16 + 4 * g4);
+              lo[0] *= f0.x; lo[1] *= f0.y; lo[2] *= f0.z; lo[3] *= f0.w;
+              hi[0] *= f1.x; hi[1] *= f1.y; hi[2] *= f1.z; hi[3] *= f1.w;
+            }
+            sB[kk] = concat(pack4(lo), pack4(hi));
+          }
+          floatx4 ax = {0.f, 0.f, 0.f, 0.f}, ao = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kk = 0; kk < KS; ++kk) {
+            const int r0 = (16 * i + l16) * KP + 32 * kk + 4 * g4;
+            const bf16x8 aq = concat(*reinterpret_cast<const bf16x4*>(buf + M::Lq + r0),
+                                     *reinterpret_cast<const bf16x4*>(buf + M::Lq + r0 + 16));
+            ao = mfma32(aq, sB[kk], ao);
+            if constexpr (kDelta) {
+              const bf16x8 ak = concat(*reinterpret_cast<const bf16x4*>(buf + M::Lk + r0),
+                                       *reinterpret_cast<const bf16x4*>(buf + M::Lk + r0 + 16));
+              ax = mfma32(ak, sB[kk], ax);
+            }
+          }
+          acc_o[i] = ao;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) yv[i][r] = kDelta ? bbeta[16 * i + 4 * g4 + r] * (vc[i][r] - ax[r]) : vc[i][r];
+        }
+        bf16x4 ub[4];
+        if constexpr (kDelta) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            floatx4 z = yv[i];
+#pragma unroll
+            for (int j = 0; j < i; ++j) {
+              const bf16x4 nl = *reinterpret_cast<const bf16x4*>(buf + M::NegL + strict_tile(i, j) * 256 + l16 * 16 +
+                                                                  4 * g4);
+              z = mfma16(nl, ub[j], z);
+            }
+            const bf16x4 ai = *reinterpret_cast<const bf16x4*>(buf + M::Ainv + i * 256 + l16 * 16 + 4 * g4);
+            const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+            ub[i] = pack4(mfma16(ai, pack4(z), zero));
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ub[i] = pack4(yv[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int j = 0; j <= i; ++j) {
+            const bf16x4 sc = *reinterpret_cast<const bf16x4*>(buf + M::Sc + tri_tile(i, j) * 256 + l16 * 16 + 4 * g4);
+            acc_o[i] = mfma16(sc, ub[j], acc_o[i]);
+          }
+        }
+        // S = diag(gamma) S + Kt^T u, Kt^T read transposed from the row-major tile
+#pragma unroll
+        for (int m = 0; m < KT; ++m) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) st[m][r] *= bgam[16 * m + 4 * g4 + r];
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+            const int tok = 32 * kk + 4 * g4 + (l16 >> 2);
+            const int chn = 16 * m + 4 * (l16 & 3);
+            const int off = (M::Kt + tok * KP + chn) * 2 + slot * M::BUF;
+            const bf16x8 ak = concat(lds_read_tr(smem, off), lds_read_tr(smem, off + 16 * KP * 2));
+            st[m] = mfma32(ak, concat(ub[2 * kk], ub[2 * kk + 1]), st[m]);
+          }
+        }
+        // output rows of chunk c
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = c * kChunk + 16 * i + 4 * g4 + r;
+            if (t < len) op[t * o_st + col] = static_cast<OutT>(scale * acc_o[i][r]);
+          }
+      }
+      __syncthreads();
+    }
+    if (a.ht) {
+#pragma unroll
+      for (int m = 0; m < KT; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a.ht[sbase + size_t(16 * m + 4 * g4 + r) * V + col] = st[m][r];
+    }
   }
 }
 
@@ -589,7 +721,7 @@ hipError_t launch_typed(const gdr_args& a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     configured = true;
   }
-  hipLaunchKernelGGL((chunk_fwd_kernel<VARIANT, K, OutT>), dim3(bh * n_slices), dim3(256), bytes, stream, a,
+  hipLaunchKernelGGL((chunk_fwd_kernel<VARIANT, K, OutT>), dim3(bh * n_slices), dim3(512), bytes, stream, a,
                      n_slices, xcd_map);
   return hipGetLastError();
 }
