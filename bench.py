@@ -32,7 +32,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PREFILL = dict(B=4, T=4096, H=16, K=128, V=128, chunk=64)
 DECODE = dict(B=256, H=16, K=128, V=128, steps=1000)
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "chunk_kda_prefill_traffic.json")
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 
 
 def delta_flops_per_token_head(C, K, V):
@@ -55,19 +55,21 @@ def decode_bytes(B, H, K, V, **_):
     return state + io
 
 
-def source_hash():
-    path = os.path.join(ROOT, "gtar-kimik3-public_amd", "csrc", "chunk.hip")
+def source_hash(source):
+    path = os.path.join(ROOT, "gtar-kimik3-public_amd", "csrc", source)
     return hashlib.sha256(open(path, "rb").read()).hexdigest()[:16]
 
 
-def committed_traffic():
+def committed_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, or None
+    when the summary was taken on a different revision of the kernel's source file."""
     try:
-        summary = json.load(open(TRAFFIC_SUMMARY))
-    except (OSError, ValueError):
+        entry = json.load(open(TRAFFIC_SUMMARY))[kernel]
+    except (OSError, ValueError, KeyError):
         return None
-    if summary.get("chunk_hip_sha256_16") != source_hash():
+    if entry.get("source_sha256_16") != source_hash(entry.get("source", "")):
         return None
-    return summary.get("hbm_bytes_per_launch")
+    return entry.get("hbm_bytes_per_launch")
 
 
 def bench_prefill(gdr, workloads, torch, steps, warmup):
@@ -122,7 +124,7 @@ def bench_decode(gdr, workloads, torch, warmup):
             "steps": cfg["steps"], "us_per_step": round(ms * 1e3, 3), "value": round(gbs, 1),
             "unit": "GB/s (state + io bytes per step)", "tokens_per_s": round(cfg["B"] / (ms * 1e-3), 1),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": committed_traffic("recurrent_kda_decode")}}
 
 
 def cpu_baseline(workloads, torch, budget_s):
@@ -154,6 +156,9 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="minimum seconds of CPU baseline work")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="after the GPU legs, copy a buffer of this many MiB three times (a plain copy kernel of "
+                         "known size that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     opts = ap.parse_args()
     if opts.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this op family runs per (sequence, head) with no cross-GPU "
@@ -190,7 +195,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": "kda_chunk_prefill", **cfg, "state": "fp32", "gate": "fp32 per-channel"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": committed_traffic()},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": committed_traffic("chunk_kda_prefill")},
         "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         "tflops": round(tflops, 2),
         "algorithmic_bytes": nbytes,
@@ -198,6 +203,12 @@ def main():
     }
     if not opts.no_decode:
         record["decode"] = bench_decode(gdr, workloads, torch, warmup=20)
+    if opts.copy_mib:
+        src = torch.ones(opts.copy_mib * 2**18, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     if not opts.no_cpu:
         record["cpu_baseline"] = cpu_baseline(workloads, torch, opts.cpu_budget)
     print(json.dumps(record), flush=True)
