@@ -28,8 +28,11 @@
 //     blocks use the block-start anchor, whose key factor e^{-b} is bounded by the block's own decay span;
 //     channels whose span exceeds kHotSpan are evaluated exactly elementwise instead (the reference always
 //     evaluates diagonal blocks elementwise, utils.py:48-53).  Gated K K^T and Q K^T strips run on bf16 MFMA
-//     (v_mfma_f32_16x16x32_bf16); each producer inverts its 16x16 diagonal block of (I + diag(beta) P) in
-//     fp32 and stores it with the off-diagonal -diag(beta) P blocks.
+//     (v_mfma_f32_16x16x32_bf16); the producers store the fp32 diagonal blocks of diag(beta) P and the
+//     off-diagonal -diag(beta) P blocks as bf16.
+//   * At the start of each step consumer wave w inverts the 16x16 unit lower-triangular diagonal block w of
+//     (I + diag(beta) P) by fp32 forward substitution (16 lanes, one column each) and publishes it through a
+//     second LDS counter, so the latency-bound substitution runs beside the producers' strips.
 //   * Consumer wave w owns 16 state columns as an fp32 [K, 16] accumulator tile in registers for the whole
 //     sequence (read from h0 once, written to ht once; no per-chunk state touches HBM).  K S and the Q S
 //     readout take the state straight from the accumulator registers as the MFMA B operand (two accumulator

@@ -89,8 +89,8 @@ int gdr_recurrent_fwd(const gdr_args* a, hipStream_t stream) {
 int gdr_chunk_fwd(const gdr_args* a, hipStream_t stream) {
   int rc = check_common(a, true);
   if (rc) return rc;
-  if (a->q.dtype != a->k.dtype || a->q.dtype != a->v.dtype)
-    return fail(GDR_ERR_INVALID, "chunk mode needs q, k, v of one dtype (got %d, %d, %d)", a->q.dtype,
+  if (a->q.dtype != GDR_BF16 || a->k.dtype != GDR_BF16 || a->v.dtype != GDR_BF16)
+    return fail(GDR_ERR_UNSUPPORTED, "chunk mode reads bf16 q, k, v (got dtype codes %d, %d, %d)", a->q.dtype,
                 a->k.dtype, a->v.dtype);
   // Rows of q, k, v, gate and out are moved with 16-byte accesses.
   const gdr_tensor* rows[] = {&a->q, &a->k, &a->v, &a->out, &a->gate};

@@ -44,20 +44,21 @@ def make_inputs(variant: str, batch: int, seq_len: int, heads: int, key_dim: int
     """Draw one seeded input set.  `gate_scale` divides the log-gates (the reference tests' gate/16 ... gate/0.1
     knob); `state_std` None means a zero (absent) initial state."""
     gen = torch.Generator("cpu").manual_seed(seed)
+    randn = lambda *shape: torch.randn(*shape, generator=gen, dtype=torch.float32)
     shape_k = (batch, seq_len, heads, key_dim)
     shape_v = (batch, seq_len, heads, value_dim)
-    query = F.normalize(torch.randn(shape_k, generator=gen), dim=-1).to(dtype)
-    key = F.normalize(torch.randn(shape_k, generator=gen), dim=-1).to(dtype)
-    value = torch.randn(shape_v, generator=gen).to(dtype)
+    query = F.normalize(randn(shape_k), dim=-1).to(dtype)
+    key = F.normalize(randn(shape_k), dim=-1).to(dtype)
+    value = randn(shape_v).to(dtype)
     gate = None
     if GATES[variant] == "channel":
-        gate = -F.softplus(torch.randn(shape_k, generator=gen)) / gate_scale
+        gate = -F.softplus(randn(shape_k)) / gate_scale
     elif GATES[variant] == "scalar":
-        gate = -F.softplus(torch.randn(batch, seq_len, heads, generator=gen)) / gate_scale
-    beta = torch.sigmoid(torch.randn(batch, seq_len, heads, generator=gen)) if BETAS[variant] else None
+        gate = -F.softplus(randn(batch, seq_len, heads)) / gate_scale
+    beta = torch.sigmoid(randn(batch, seq_len, heads)) if BETAS[variant] else None
     state = None
     if state_std is not None:
-        state = torch.randn(batch, heads, key_dim, value_dim, generator=gen) * state_std
+        state = randn(batch, heads, key_dim, value_dim) * state_std
 
     def place(x):
         if x is None:
@@ -82,5 +83,5 @@ def decode_state(batch: int, heads: int, key_dim: int, value_dim: int, *, std: f
     gen = torch.Generator("cpu").manual_seed(seed)
     out = torch.empty(batch, heads, key_dim, value_dim, dtype=torch.float32, device=device)
     for b in range(batch):
-        out[b].copy_(torch.randn(heads, key_dim, value_dim, generator=gen) * std)
+        out[b].copy_(torch.randn(heads, key_dim, value_dim, generator=gen, dtype=torch.float32) * std)
     return out

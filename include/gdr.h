@@ -80,7 +80,8 @@ typedef struct gdr_args {
  *   ChunkGatedLinearAttention   src/ops/gated_linear_attention.py:362-384
  *   ChunkDeltaNet               src/ops/deltanet.py:326-347
  * (pad_sequence + chunk_cumsum + kernel matrices + WY representation + state scan + output, six launches and
- * a [B,H,NC+1,K,V] States buffer in the reference) with one fused launch.  q, k, v must share one dtype.
+ * a [B,H,NC+1,K,V] States buffer in the reference) with one fused launch.  q, k, v must be bf16 (the MFMA
+ * operand type; the Python layer casts); out may be bf16, f16 or f32.
  * Supports K in {64, 128}, V a multiple of 64, any T >= 1, and packed varlen input through cu_seqlens. */
 int gdr_chunk_fwd(const gdr_args* args, hipStream_t stream);
 

@@ -15,7 +15,15 @@ import torch.nn.functional as F
 
 from _helpers import oracle
 
-torch.set_default_dtype(torch.float64)
+
+
+@pytest.fixture(autouse=True)
+def _float64_default():
+    """The pins run in float64; the default dtype is restored so other test modules are unaffected."""
+    previous = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(previous)
 
 
 def _rand_inputs(variant, B=2, H=2, T=12, K=4, V=3, seed=0, gate_scale=1.0, state=True):
