@@ -95,6 +95,9 @@ def run(variant: int, chunk: bool, query, key, value, gate, beta, scale, initial
             raise ValueError(f"{name}: initial_state must have shape {state_shape}, got {tuple(initial_state.shape)}")
         initial_state = initial_state.float().contiguous()
 
+    if not chunk and not (query.dtype == key.dtype == value.dtype == torch.bfloat16):
+        # The recurrent kernel reads q, k, v as one element type: all bf16, or else all fp32 (an exact widening).
+        query, key, value = (x if x.dtype == torch.float32 else x.float() for x in (query, key, value))
     if chunk:
         # The chunk kernel runs its matrix products in bf16 on MFMA; it reads bf16 q, k, v with 16-byte rows.
         query, key, value = (x.to(torch.bfloat16) for x in (query, key, value))

@@ -80,6 +80,9 @@ const char* gdr_last_error(void) { return g_last_error.c_str(); }
 int gdr_recurrent_fwd(const gdr_args* a, hipStream_t stream) {
   int rc = check_common(a, false);
   if (rc) return rc;
+  if (a->q.dtype != a->k.dtype || a->q.dtype != a->v.dtype || a->q.dtype == GDR_F16)
+    return fail(GDR_ERR_UNSUPPORTED, "recurrent mode reads q, k, v of one dtype, bf16 or f32 (got dtype codes %d, %d, %d)",
+                a->q.dtype, a->k.dtype, a->v.dtype);
   hipError_t e = gdr::launch_recurrent(*a, stream);
   if (e != hipSuccess) return fail(GDR_ERR_HIP, "recurrent launch failed: %s", hipGetErrorString(e));
   g_last_error.clear();

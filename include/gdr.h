@@ -90,7 +90,8 @@ int gdr_chunk_fwd(const gdr_args* args, hipStream_t stream);
  *   recurrent_gated_deltanet           src/ops/gated_deltanet.py:497-520 (kernel :29-59)
  *   recurrent_gated_linear_attention   src/ops/gated_linear_attention.py:461-483 (kernel :30-56)
  *   recurrent_deltanet                 src/ops/deltanet.py:423-445 (kernel :30-57)
- * Supports K in {64, 128}, V a multiple of 32, any T >= 1 (cu_seqlens must be NULL). */
+ * q, k, v must share one dtype, bf16 or f32 (the Python layer widens mixed or f16 inputs to f32, exactly); out may
+ * be bf16, f16 or f32.  Supports K in {64, 128}, V a multiple of 32, any T >= 1 (cu_seqlens must be NULL). */
 int gdr_recurrent_fwd(const gdr_args* args, hipStream_t stream);
 
 /* Thread-local description of the calling thread's last failure ("" if none).  No reference counterpart:
