@@ -108,5 +108,6 @@ def run(variant: int, chunk: bool, query, key, value, gate, beta, scale, initial
     out = torch.empty(batch, heads, seq_len, value_dim, device=device, dtype=out_dtype)
     final_state = torch.empty(state_shape, device=device, dtype=torch.float32) if output_final_state else None
     args = _lib.make_args(variant, query, key, value, gate, beta, out, scale, initial_state, final_state, cu_seqlens)
+    workspace = _lib.chunk_workspace(args, device) if chunk else None  # noqa: F841 (alive until enqueued)
     _lib.launch("gdr_chunk_fwd" if chunk else "gdr_recurrent_fwd", args, device)
     return (out, final_state) if output_final_state else out

@@ -18,7 +18,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.join(_HERE, "libgdr.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 KDA, GDN, GLA, DELTANET = 0, 1, 2, 3
 F32, BF16, F16 = 0, 1, 2
@@ -57,12 +57,15 @@ class GdrArgs(ctypes.Structure):
         ("cu_seqlens", ctypes.c_void_p),
         ("n_seqs", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
     ]
 
 
 # Every symbol include/gdr.h declares, with its ctypes signature.
 EXPORTS = {
     "gdr_chunk_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
+    "gdr_chunk_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(GdrArgs)]),
     "gdr_recurrent_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
     "gdr_last_error": (ctypes.c_char_p, []),
     "gdr_abi_version": (ctypes.c_int, []),
@@ -129,6 +132,19 @@ def make_args(variant, q, k, v, gate, beta, out, scale, h0, ht, cu_seqlens=None)
         args.cu_seqlens = cu_seqlens.data_ptr()
         args.n_seqs = cu_seqlens.numel() - 1
     return args
+
+
+def chunk_workspace(args: GdrArgs, device: torch.device) -> torch.Tensor:
+    """Allocate (from torch's caching allocator) and attach the chunk-mode workspace; keep the returned tensor
+    alive until the launch has been enqueued."""
+    lib = load_library()
+    nbytes = lib.gdr_chunk_workspace_bytes(ctypes.byref(args))
+    if nbytes < 0:
+        raise RuntimeError(f"gdr_chunk_workspace_bytes failed ({nbytes}): {lib.gdr_last_error().decode()}")
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = int(nbytes)
+    return ws
 
 
 def launch(entry: str, args: GdrArgs, device: torch.device) -> None:

@@ -1,0 +1,726 @@
+// Chunkwise (prefill) forward of the gated delta-rule family on gfx950 in two launches: a chunk-parallel
+// preparation kernel and a sequential state-scan kernel, joined by a workspace in HBM.
+//
+// Reference: the forward of ChunkKimiDeltaAttention (src/ops/kimi_delta_attention.py:535-558) -- chunk_cumsum
+// (utils.py:15-23), kernel matrices (:71-106), WY representation (:109-136), state scan (:139-170), output
+// (:173-197) -- and its Gated DeltaNet / GLA / DeltaNet twins (gated_deltanet.py:62-162,
+// gated_linear_attention.py:59-144, deltanet.py:60-149).
+//
+// Per chunk of C = 64 tokens with state S entering it (B = in-chunk inclusive cumsum of the log gate):
+//   P = tril(K K^T (x) e^{B_t - B_s}, -1),   A = (I + diag(beta) P)^{-1}
+//   W = A diag(beta) K e^B,   U = A diag(beta) V          (GLA: no W, U = V)
+//   u = U - W S,   O = scale [(Q e^B) S + tril(Q K^T (x) e^{B_t - B_s}) u],   S' = diag(e^{B_end}) S + (K e^{B_end - B})^T u
+//
+// Everything that does not depend on S is chunk-local, so it runs in `chunk_prep_kernel` with one workgroup per
+// (chunk, head): thousands of independent workgroups that fill all 256 CUs.  The prep kernel writes one record
+// per (chunk, head) -- W, Q e^B, (K e^{B_end - B})^T, the ten gated score tiles, e^{B_end} and U^T -- laid out
+// exactly as the scan kernel's LDS image, so the scan kernel stages a record with straight 16-byte copies.
+// `chunk_scan_kernel` keeps the fp32 state of one (sequence, head) x 64-column slice in the registers of four
+// compute waves for the whole sequence and per chunk runs only MFMA work: X = W S and Q e^B S (bf16, 32-deep),
+// u = U - X, the intra-chunk output Sc u and the state update; four loader waves stream the next chunk's record
+// into the other half of a double-buffered LDS region meanwhile.  The per-chunk critical path has no triangular
+// solve and no transcendental: those are all in the prep kernel.
+//
+// Numerics of the prep kernel: decay factors are anchored per 16-row block so that every factor folded into a
+// bf16 MFMA operand of the gated K K^T / Q K^T strips is <= 1, except the diagonal-tile key factor e^{-T_i},
+// which is bounded by the block's own decay span; channels whose span exceeds kHotSpan are evaluated exactly
+// elementwise instead (the reference evaluates diagonal blocks elementwise, utils.py:48-53).  The diagonal
+// 16x16 blocks of (I + diag(beta) P) are inverted in fp32; W and U come out of a blocked forward substitution on
+// v_mfma_f32_16x16x16_bf16 with fp32 accumulation.  W, U, Q e^B and K e^{B_end - B} are stored as bf16, as the
+// reference stores W, U and u.
+#include "chunk_common.h"
+#include "gdr_internal.h"
+
+namespace gdr {
+
+using namespace chunk;
+
+namespace {
+
+constexpr int kScanSlice = 64;  // value columns per scan workgroup
+
+// Workspace record of one (chunk, head); byte offsets.  UT (U^T, [V][TP]) closes the record.
+template <int K>
+struct Rec {
+  static constexpr int KP = K + 8;   // row pitch of [64][K] bf16 arrays (16-byte skew per row)
+  static constexpr int TP = 64 + 8;  // row pitch of [*][64 tokens] bf16 arrays
+  static constexpr int W = 0;                                   // bf16 [64][KP]  A diag(beta) K e^B
+  static constexpr int QD = W + 64 * KP * 2;                    // bf16 [64][KP]  Q e^B
+  static constexpr int KT = QD + 64 * KP * 2;                   // bf16 [64][KP]  K e^{B_end - B}
+  static constexpr int SC = KT + 64 * KP * 2;                   // bf16 [10][16][16] gated scores, tile (i, j <= i)
+  static constexpr int GAM = SC + 10 * 256 * 2;                 // fp32 [K] e^{B_end}
+  static constexpr int FIX = ((GAM + K * 4 + 255) / 256) * 256;  // start of UT
+  static constexpr int UT_SLICE = kScanSlice * TP * 2;          // bytes of 64 rows of UT
+  static int64_t bytes(int value_dim) { return FIX + ((int64_t(value_dim) * TP * 2 + 255) / 256) * 256; }
+};
+
+// LDS of the prep kernel (bytes); 3 workgroups fit a CU for K = 128.
+template <int K>
+struct PrepLds {
+  static constexpr int KP = K + 8;
+  static constexpr int KAP = 0;                   // bf16 [64][KP] k e^{a_p - b}  (block-end anchor, strip keys)
+  static constexpr int AINV = KAP;                // bf16 [4][256] (I + diag(beta) P_ii)^{-1}, after the strips
+  static constexpr int KD = KAP + 64 * KP * 2;    // bf16 [64][KP] k e^B         (right-hand side of the solve)
+  static constexpr int SC = KD + 64 * KP * 2;     // bf16 [10][256] gated score tiles
+  static constexpr int NEGL = SC + 10 * 512;      // bf16 [6][256]  -diag(beta) P, tile (i, j < i)
+  static constexpr int LII = NEGL + 6 * 512;      // fp32 [4][256]  diag(beta) P_ii (strictly lower)
+  static constexpr int TOT = LII + 4 * 1024;      // fp32 [4][K]    per-block log2-gate totals
+  static constexpr int RDS = TOT + 4 * K * 4;     // fp32 [4][K]    diagonal key factor e^{-T_i} (0: hot channel)
+  static constexpr int FAR = RDS + 4 * K * 4;     // fp32 [3][K]    key factors of tiles (2,0), (3,0), (3,1)
+  static constexpr int BETA = FAR + 3 * K * 4;    // fp32 [64]
+  static constexpr int BYTES = BETA + 256;
+};
+
+// Four consecutive outputs (scaled) in one 8-byte (16-bit types) or 16-byte (fp32) store.
+__device__ __forceinline__ void store4(__bf16* dst, floatx4 v, float s) {
+  *reinterpret_cast<bf16x4*>(dst) = bf16x4{bf(v[0] * s), bf(v[1] * s), bf(v[2] * s), bf(v[3] * s)};
+}
+__device__ __forceinline__ void store4(_Float16* dst, floatx4 v, float s) {
+  typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4;
+  *reinterpret_cast<f16x4*>(dst) = f16x4{static_cast<_Float16>(v[0] * s), static_cast<_Float16>(v[1] * s),
+                                         static_cast<_Float16>(v[2] * s), static_cast<_Float16>(v[3] * s)};
+}
+__device__ __forceinline__ void store4(float* dst, floatx4 v, float s) {
+  *reinterpret_cast<float4*>(dst) = make_float4(v[0] * s, v[1] * s, v[2] * s, v[3] * s);
+}
+
+// First workspace slot of packed sequence n: floor(bos / 64) + n.  Slots of consecutive sequences never
+// overlap (floor(a + b) >= floor(a) + floor(b) and floor(len / 64) + 1 >= ceil(len / 64)) and every slot is below
+// ceil(T / 64) + n_seqs.
+__device__ __forceinline__ int varlen_base(const int32_t* cu, int n) { return cu[n] / kChunk + n; }
+
+// ======================================= prep: one workgroup per (chunk, head) =======================================
+template <int VARIANT, int K>
+__global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int nc, int64_t rec_bytes) {
+  constexpr bool kDelta = VARIANT != GDR_GLA;
+  constexpr int kGate = (VARIANT == GDR_KDA || VARIANT == GDR_GLA) ? 2 : (VARIANT == GDR_GDN ? 1 : 0);
+  constexpr int KS = K / 32;
+  using L = PrepLds<K>;
+  using R = Rec<K>;
+  constexpr int KP = L::KP, TP = R::TP;
+  constexpr float kHot = kHotSpan * kLog2e;  // hot threshold on -T in log2 units
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  // ---- workgroup -> (sequence n, head h, chunk c) ----
+  const int H = a.heads;
+  const int h = blockIdx.x % H, slot = blockIdx.x / H;
+  int n, c, bos = 0, len = a.seq_len;
+  if (a.cu_seqlens) {
+    int lo = 0, hi = a.n_seqs - 1;  // largest n with base(n) <= slot
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (varlen_base(a.cu_seqlens, mid) <= slot) lo = mid; else hi = mid - 1;
+    }
+    n = lo;
+    bos = a.cu_seqlens[n];
+    len = a.cu_seqlens[n + 1] - bos;
+    c = slot - varlen_base(a.cu_seqlens, n);
+    if (c < 0 || c * kChunk >= len) return;  // gap slot: uniform over the workgroup, before any barrier
+  } else {
+    n = slot / nc;
+    c = slot % nc;
+  }
+  const int bidx = a.cu_seqlens ? 0 : n;
+  ChunkCtx x;
+  x.q_st = a.q.stride_t; x.k_st = a.k.stride_t; x.v_st = a.v.stride_t; x.o_st = 0;
+  x.g_st = a.gate.stride_t; x.b_st = a.beta.stride_t;
+  x.qp = static_cast<const __bf16*>(a.q.ptr) + bidx * a.q.stride_b + h * a.q.stride_h + bos * x.q_st;
+  x.kp = static_cast<const __bf16*>(a.k.ptr) + bidx * a.k.stride_b + h * a.k.stride_h + bos * x.k_st;
+  x.vp = static_cast<const __bf16*>(a.v.ptr) + bidx * a.v.stride_b + h * a.v.stride_h + bos * x.v_st;
+  x.gp = kGate ? static_cast<const float*>(a.gate.ptr) + bidx * a.gate.stride_b + h * a.gate.stride_h + bos * x.g_st
+               : nullptr;
+  x.betap = kDelta ? static_cast<const float*>(a.beta.ptr) + bidx * a.beta.stride_b + h * a.beta.stride_h +
+                         bos * x.b_st
+                   : nullptr;
+  x.op = nullptr;
+  x.len = len;
+  x.nchunks = 0; x.v0 = 0; x.V = a.value_dim; x.sbase = 0; x.h0 = nullptr; x.ht = nullptr; x.scale = 0.f;
+  unsigned char* rec = static_cast<unsigned char*>(a.workspace) + (int64_t(slot) * H + h) * rec_bytes;
+
+  __bf16* kap = reinterpret_cast<__bf16*>(smem + L::KAP);
+  __bf16* ainv = reinterpret_cast<__bf16*>(smem + L::AINV);
+  __bf16* kd = reinterpret_cast<__bf16*>(smem + L::KD);
+  __bf16* sct = reinterpret_cast<__bf16*>(smem + L::SC);
+  __bf16* negl = reinterpret_cast<__bf16*>(smem + L::NEGL);
+  float* lii = reinterpret_cast<float*>(smem + L::LII);
+  float* tot = reinterpret_cast<float*>(smem + L::TOT);
+  float* rds = reinterpret_cast<float*>(smem + L::RDS);
+  float* far = reinterpret_cast<float*>(smem + L::FAR);
+  float* sbeta = reinterpret_cast<float*>(smem + L::BETA);
+
+  // A-operand lane layout: lane (l16, g4) of wave p holds row 16 p + l16, channels 32 kk + 8 g4 + j.
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, g4 = lane >> 4;
+  const int p = wave;
+  const int crow = c * kChunk + 16 * p + l16;  // token index within the sequence
+  const bool valid = crow < len;
+  const int tc = min(crow, len - 1);
+
+  // ---- 1. loads: this lane's q, k, gate, beta row; the value rows of the wave's first U tile ----
+  uint4 qraw[KS], kraw[KS];
+  float bl[KS][8];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    const int ch = 32 * kk + 8 * g4;
+    qraw[kk] = *reinterpret_cast<const uint4*>(x.qp + tc * x.q_st + ch);
+    kraw[kk] = *reinterpret_cast<const uint4*>(x.kp + tc * x.k_st + ch);
+    if constexpr (kGate == 2) {
+      const float4 g0 = *reinterpret_cast<const float4*>(x.gp + tc * x.g_st + ch);
+      const float4 g1 = *reinterpret_cast<const float4*>(x.gp + tc * x.g_st + ch + 4);
+      bl[kk][0] = g0.x; bl[kk][1] = g0.y; bl[kk][2] = g0.z; bl[kk][3] = g0.w;
+      bl[kk][4] = g1.x; bl[kk][5] = g1.y; bl[kk][6] = g1.z; bl[kk][7] = g1.w;
+    }
+  }
+  if constexpr (kGate == 1) {
+    const float g = x.gp[tc * x.g_st];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bl[kk][j] = g;
+  }
+  if constexpr (kGate == 0) {
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bl[kk][j] = 0.f;
+  }
+  const float beta_t = kDelta ? x.betap[tc * x.b_st] : 0.f;
+
+  const int kt_tiles = kDelta ? K / 16 : 0, n_tiles = kt_tiles + a.value_dim / 16;
+  // Value rows of the wave's next U tile (D layout: rows 16 i + 4 g4 + r, column col), fetched one tile ahead so
+  // a global load is never waited on right after it is issued.
+  uint32_t vnext[4][4];
+  auto fetch_v = [&](int nt) {
+    const int col = 16 * (nt - kt_tiles) + l16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = min(c * kChunk + 16 * i + 4 * g4 + r, len - 1);
+        vnext[i][r] = reinterpret_cast<const uint16_t*>(x.vp)[t * x.v_st + col];
+      }
+  };
+  int first_u = wave;
+  while (first_u < kt_tiles) first_u += 4;
+  if (first_u < n_tiles) fetch_v(first_u);
+
+  // ---- 2. in-block inclusive cumsum of the log2 gate over the 16 rows (lanes l16); block totals ----
+  float tw[KS][8];
+  if constexpr (kGate) {
+    const float keep = valid ? kLog2e : 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bl[kk][j] *= keep;
+#pragma unroll
+    for (int off = 1; off < 16; off *= 2) {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float y = __shfl_up(bl[kk][j], off, 16);
+          if (l16 >= off) bl[kk][j] += y;
+        }
+    }
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tw[kk][j] = __shfl(bl[kk][j], 15, 16);
+    if (l16 == 15) {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        float* dst = tot + p * K + 32 * kk + 8 * g4;
+        *reinterpret_cast<float4*>(dst) = make_float4(bl[kk][0], bl[kk][1], bl[kk][2], bl[kk][3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(bl[kk][4], bl[kk][5], bl[kk][6], bl[kk][7]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tw[kk][j] = 0.f;
+  }
+  if (g4 == 0) sbeta[16 * p + l16] = valid ? beta_t : 0.f;
+  lds_barrier();
+
+  // ---- 3a. key factors of the strips, spread over the workgroup: RDS[i] = e^{-T_i} (0 for a hot channel),
+  // FAR = e^{a_{i-1} - a_j} for the far tiles (2,0), (3,0), (3,1) ----
+  if constexpr (kGate) {
+    for (int idx = threadIdx.x; idx < 7 * K; idx += 256) {
+      const int v = idx / K, ch = idx % K;
+      if (v < 4) {
+        const float t = tot[v * K + ch];
+        rds[v * K + ch] = -t > kHot ? 0.f : __builtin_amdgcn_exp2f(-t);
+      } else {
+        const float e = v == 4 ? tot[K + ch] : (v == 5 ? tot[K + ch] + tot[2 * K + ch] : tot[2 * K + ch]);
+        far[(v - 4) * K + ch] = __builtin_amdgcn_exp2f(e);
+      }
+    }
+  }
+  // ---- 3b. operands.  Block anchors a_{p-1} (pre) and a_p = a_{p-1} + T_p; chunk-end tail = B_end - a_p ----
+  bf16x8 lq[KS], lk[KS];
+  const uint32_t keep_bits = valid ? 0xffffffffu : 0u;
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    const int ch = 32 * kk + 8 * g4;
+    float qf[8], kf[8];
+    unpack8(make_uint4(qraw[kk].x & keep_bits, qraw[kk].y & keep_bits, qraw[kk].z & keep_bits,
+                       qraw[kk].w & keep_bits), qf);
+    unpack8(make_uint4(kraw[kk].x & keep_bits, kraw[kk].y & keep_bits, kraw[kk].z & keep_bits,
+                       kraw[kk].w & keep_bits), kf);
+    float pre[8], tail[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pre[j] = tail[j] = 0.f;
+    if constexpr (kGate) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m == p) continue;
+        const float4 t0 = *reinterpret_cast<const float4*>(tot + m * K + ch);
+        const float4 t1 = *reinterpret_cast<const float4*>(tot + m * K + ch + 4);
+        const float tv[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (m < p) pre[j] += tv[j];
+          else tail[j] += tv[j];
+        }
+      }
+    }
+    bf16x8 vq, vk, vkap, vkd, vkt, vqd;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float ell = 1.f, rho = 1.f, epre = 1.f, etail = 1.f;
+      if constexpr (kGate) {
+        ell = __builtin_amdgcn_exp2f(bl[kk][j]);
+        rho = __builtin_amdgcn_exp2f(tw[kk][j] - bl[kk][j]);
+        epre = __builtin_amdgcn_exp2f(pre[j]);
+        etail = __builtin_amdgcn_exp2f(tail[j]);
+      }
+      const float q1 = qf[j] * ell, k1 = kf[j] * ell, kp1 = kf[j] * rho;
+      vq[j] = bf(q1);
+      vk[j] = bf(k1);
+      vkap[j] = bf(kp1);
+      vkd[j] = bf(k1 * epre);
+      vkt[j] = bf(kp1 * etail);
+      vqd[j] = bf(q1 * epre);
+    }
+    lq[kk] = vq;
+    lk[kk] = vk;
+    const int ro = (16 * p + l16) * KP + ch;
+    *reinterpret_cast<bf16x8*>(kap + ro) = vkap;
+    if constexpr (kDelta) *reinterpret_cast<bf16x8*>(kd + ro) = vkd;
+    *reinterpret_cast<bf16x8*>(rec + R::QD + ro * 2) = vqd;  // Q e^B
+    *reinterpret_cast<bf16x8*>(rec + R::KT + ro * 2) = vkt;  // K e^{B_end - B}
+  }
+  lds_barrier();
+
+  // ---- 4. gated strips of block row p: tiles (p, j <= p) of Sc and P ----
+  for (int j = 0; j <= p; ++j) {
+    floatx4 acc_s = {0.f, 0.f, 0.f, 0.f}, acc_p = {0.f, 0.f, 0.f, 0.f};
+    const bool diag = j == p, adjacent = j + 1 == p;
+    const float* kscale = diag ? rds + p * K : far + ((p == 2) ? 0 : (j == 0 ? 1 : 2)) * K;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      const int ch = 32 * kk + 8 * g4;
+      bf16x8 bk = *reinterpret_cast<const bf16x8*>(kap + (16 * j + l16) * KP + ch);
+      if (kGate && !adjacent) {
+        const float4 f0 = *reinterpret_cast<const float4*>(kscale + ch);
+        const float4 f1 = *reinterpret_cast<const float4*>(kscale + ch + 4);
+        const float f[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bk[e] = bf(f32(bk[e]) * f[e]);
+      }
+      acc_s = mfma32(lq[kk], bk, acc_s);
+      if constexpr (kDelta) acc_p = mfma32(lk[kk], bk, acc_p);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 4 * g4 + r, sl = l16;
+      sct[tri_tile(p, j) * 256 + t * 16 + sl] = bf(diag && t < sl ? 0.f : acc_s[r]);
+      if constexpr (kDelta) {
+        const float pv = acc_p[r] * sbeta[16 * p + t];
+        if (diag) lii[p * 256 + t * 16 + sl] = t > sl ? pv : 0.f;
+        else negl[strict_tile(p, j) * 256 + t * 16 + sl] = bf(-pv);
+      }
+    }
+  }
+  // exact elementwise diagonal block for hot channels (rare)
+  if constexpr (kGate) {
+    constexpr int LPR = K / 8;
+    const int cgh = lane % LPR;
+    uint32_t hot_mask = 0;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) hot_mask |= (-tot[p * K + 8 * cgh + m] > kHot) ? (1u << m) : 0u;
+    if (__any(hot_mask != 0)) {
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      hot_diag_fixup<K, kDelta, kGate, 0>(x, c * kChunk, p, hot_mask, sct + tri_tile(p, p) * 256, lii + p * 256,
+                                          sbeta + 16 * p);
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      hot_diag_fixup<K, kDelta, kGate, 4>(x, c * kChunk, p, hot_mask, sct + tri_tile(p, p) * 256, lii + p * 256,
+                                          sbeta + 16 * p);
+    }
+  }
+  lds_barrier();
+
+  // ---- 5. diagonal inverses (wave p, 16 lanes, fp32 forward substitution); score tiles and e^{B_end} out ----
+  if constexpr (kDelta) {
+    if (lane < 16) {
+      const float* lt = lii + p * 256;
+      float xcol[16];
+      xcol[0] = lane == 0 ? 1.f : 0.f;
+#pragma unroll
+      for (int r = 1; r < 16; ++r) {
+        float lrow[16];
+#pragma unroll
+        for (int m4 = 0; m4 < (r + 3) / 4; ++m4) {
+          const float4 v = *reinterpret_cast<const float4*>(lt + r * 16 + 4 * m4);
+          lrow[4 * m4] = v.x; lrow[4 * m4 + 1] = v.y; lrow[4 * m4 + 2] = v.z; lrow[4 * m4 + 3] = v.w;
+        }
+        float acc0 = (r == lane) ? 1.f : 0.f, acc1 = 0.f;
+#pragma unroll
+        for (int m = 0; m < r; m += 2) {
+          acc0 -= lrow[m] * xcol[m];
+          if (m + 1 < r) acc1 -= lrow[m + 1] * xcol[m + 1];
+        }
+        xcol[r] = acc0 + acc1;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ainv[p * 256 + r * 16 + lane] = bf(xcol[r]);
+    }
+  }
+  for (int i = threadIdx.x; i < 10 * 256 * 2 / 16; i += 256)
+    reinterpret_cast<uint4*>(rec + R::SC)[i] = reinterpret_cast<const uint4*>(sct)[i];
+  if (threadIdx.x < K) {
+    float b_end = 0.f;
+    if constexpr (kGate)
+      b_end = tot[threadIdx.x] + tot[K + threadIdx.x] + tot[2 * K + threadIdx.x] + tot[3 * K + threadIdx.x];
+    reinterpret_cast<float*>(rec + R::GAM)[threadIdx.x] = kGate ? __builtin_amdgcn_exp2f(b_end) : 1.f;
+  }
+  lds_barrier();
+
+  // ---- 6. [W | U] = A diag(beta) [K e^B | V] by blocked forward substitution; wave w owns N-tiles w, w+4, ...
+  // Block i: Y_i = diag(beta_i) R_i - sum_{j<i} L_ij X_j,  X_i = A_ii Y_i.  X_i (accumulator layout: rows 4 g4 + r,
+  // column l16) feeds the later blocks; for W the transposed product X_i^T = Y_i^T A_ii^T (the same two operands
+  // with their roles swapped) puts four consecutive channels of one row in each lane for 8-byte row stores. ----
+  __bf16* wrec = reinterpret_cast<__bf16*>(rec + R::W);
+  __bf16* utrec = reinterpret_cast<__bf16*>(rec + R::FIX);
+  const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  for (int nt = wave; nt < n_tiles; nt += 4) {
+    const bool is_w = nt < kt_tiles;
+    const int col0 = 16 * (is_w ? nt : nt - kt_tiles);
+    float vcur[4][4];
+    if (!is_w) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          vcur[i][r] = c * kChunk + 16 * i + 4 * g4 + r < len ? bf16_bits_to_f32(uint16_t(vnext[i][r])) : 0.f;
+      if (nt + 4 < n_tiles) fetch_v(nt + 4);
+    }
+    bf16x4 xs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      floatx4 z;
+      if (is_w) {
+        // K e^B rows 16 i + 4 g4 + r, column col0 + l16, with one transposing read
+        const int off = L::KD + ((16 * i + 4 * g4 + (l16 >> 2)) * KP + col0 + 4 * (l16 & 3)) * 2;
+        const bf16x4 kv = lds_read_tr(smem, off);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = f32(kv[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = vcur[i][r];
+      }
+      if constexpr (kDelta) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] *= sbeta[16 * i + 4 * g4 + r];
+#pragma unroll
+        for (int j = 0; j < i; ++j) {
+          const bf16x4 nl = *reinterpret_cast<const bf16x4*>(negl + strict_tile(i, j) * 256 + l16 * 16 + 4 * g4);
+          z = mfma16(nl, xs[j], z);
+        }
+        const bf16x4 ai = *reinterpret_cast<const bf16x4*>(ainv + i * 256 + l16 * 16 + 4 * g4);
+        const bf16x4 zb = pack4(z);
+        xs[i] = pack4(mfma16(ai, zb, zero4));
+        if (is_w) {
+          const bf16x4 xt = pack4(mfma16(zb, ai, zero4));  // X_i^T: row 16 i + l16, channels col0 + 4 g4 + r
+          *reinterpret_cast<bf16x4*>(wrec + (16 * i + l16) * KP + col0 + 4 * g4) = xt;
+        }
+      } else {
+        xs[i] = pack4(z);
+      }
+      if (!is_w) *reinterpret_cast<bf16x4*>(utrec + (col0 + l16) * TP + 16 * i + 4 * g4) = xs[i];
+    }
+  }
+}
+
+// =============================== scan: one workgroup per (sequence, head) x 64 columns ===============================
+constexpr int kScanTiles = 1;                          // 16-column tiles per compute wave
+constexpr int kScanCompute = kScanSlice / (16 * kScanTiles);  // compute waves per scan workgroup
+constexpr int kScanLoaders = 2;                        // loader waves per scan workgroup
+constexpr int kScanThreads = 64 * (kScanCompute + kScanLoaders);
+
+template <int VARIANT, int K, typename OutT>
+__global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_args a, int n_slices, int xcd_map,
+                                                                     int nc, int64_t rec_bytes) {
+  constexpr bool kDelta = VARIANT != GDR_GLA;
+  constexpr int KT = K / 16, KS = K / 32, NT = kScanTiles;
+  using R = Rec<K>;
+  constexpr int KP = R::KP, TP = R::TP;
+  constexpr int SB = R::FIX + R::UT_SLICE;         // LDS bytes per buffer
+  constexpr int NF = R::FIX / 16, NU = R::UT_SLICE / 16;
+  constexpr int NG = ((NF + NU + 63) / 64 + kScanLoaders - 1) / kScanLoaders;  // 64-piece groups per loader wave
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int xb = blockIdx.x;
+  int bh, slice;
+  if (xcd_map) {
+    const int xcd = xb & 7, local = xb >> 3;
+    slice = local % n_slices;
+    bh = (local / n_slices) * 8 + xcd;
+  } else {
+    slice = xb % n_slices;
+    bh = xb / n_slices;
+  }
+  const int H = a.heads;
+  const int n = bh / H, h = bh % H;
+  int bos = 0, len = a.seq_len, base = n * nc, bidx = n;
+  if (a.cu_seqlens) {
+    bos = a.cu_seqlens[n];
+    len = a.cu_seqlens[n + 1] - bos;
+    base = varlen_base(a.cu_seqlens, n);
+    bidx = 0;
+  }
+  const int nchunks = (len + kChunk - 1) / kChunk;
+  const int v0 = slice * kScanSlice;
+  const unsigned char* ws = static_cast<const unsigned char*>(a.workspace);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+
+  if (wave >= kScanCompute) {
+    // ---------------- loader waves ----------------
+    // The record of chunk s + 1 is copied straight into LDS buffer (s + 1) & 1 while the compute waves work on
+    // chunk s (global_load_lds_dwordx4: each lane's 16 bytes land at the wave-uniform LDS base + 16 * lane).
+    const int lw = wave - kScanCompute;
+    const unsigned char* rec0 = ws + (int64_t(base) * H + h) * rec_bytes;
+    const int64_t rec_stride = int64_t(H) * rec_bytes;
+    const int ut_off = R::FIX + v0 * TP * 2;
+    auto copy_record = [&](int chunk, int buf) {
+      const unsigned char* src = rec0 + chunk * rec_stride;
+      unsigned char* dst = smem + buf * SB;
+#pragma unroll
+      for (int k = 0; k < NG; ++k) {
+        const int g = lw + kScanLoaders * k;  // group of 64 16-byte pieces
+        const int idx = 64 * g + lane;
+        if (idx < NF + NU) {
+          const int off = idx < NF ? idx * 16 : ut_off + (idx - NF) * 16;
+          __builtin_amdgcn_global_load_lds(src + off, (__attribute__((address_space(3))) void*)(dst + 1024 * g),
+                                           16, 0, 0);
+        }
+      }
+    };
+    if (nchunks > 0) copy_record(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
+    for (int s = 0; s < nchunks; ++s) {
+      if (s + 1 < nchunks) copy_record(s + 1, (s + 1) & 1);  // buffer (s + 1) & 1 held chunk s - 1: done
+      __builtin_amdgcn_s_waitcnt(0);
+      lds_barrier();
+    }
+    return;
+  }
+
+  // ---------------- compute waves: NT 16-column tiles each ----------------
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int c0 = v0 + 16 * NT * wave;  // first column of this wave
+  const size_t sbase = size_t(n * H + h) * K * a.value_dim;
+  OutT* op = static_cast<OutT*>(const_cast<void*>(a.out.ptr)) + bidx * a.out.stride_b + h * a.out.stride_h +
+             bos * a.out.stride_t;
+  const int64_t o_st = a.out.stride_t;
+  floatx4 st[NT][KT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int m = 0; m < KT; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        st[t][m][r] = a.h0 ? a.h0[sbase + size_t(16 * m + 4 * g4 + r) * a.value_dim + c0 + 16 * t + l16] : 0.f;
+  lds_barrier();
+
+  for (int s = 0; s < nchunks; ++s) {
+    const unsigned char* bb = smem + (s & 1) * SB;
+    const __bf16* wl = reinterpret_cast<const __bf16*>(bb + R::W);
+    const __bf16* ql = reinterpret_cast<const __bf16*>(bb + R::QD);
+    const __bf16* scl = reinterpret_cast<const __bf16*>(bb + R::SC);
+    const float* gam = reinterpret_cast<const float*>(bb + R::GAM);
+    const __bf16* utl = reinterpret_cast<const __bf16*>(bb + R::FIX) + (c0 - v0 + l16) * TP;
+
+    // state as the bf16 B operand: two accumulator tiles = one 32-deep k slot set {32kk + 4g4 + r, +16}
+    bf16x8 sB[NT][KS];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) sB[t][kk] = concat(pack4(st[t][2 * kk]), pack4(st[t][2 * kk + 1]));
+
+    // X = W S (accumulator layout: token rows, state columns) and the transposed readout (Q e^B S)^T = S^T (Q e^B)^T
+    // (the same operands with their roles swapped: state-column rows, token columns), so that each lane ends up
+    // with four consecutive output columns of one token.  Every A fragment read from LDS feeds NT tiles.
+    floatx4 acc_ot[NT][4];
+    bf16x4 ub[NT][4];
+    // A fragments of row block i (Q e^B and W, k slots {32kk + 4g4 + r, +16}), read one block ahead
+    bf16x8 fq[2][KS], fw[2][KS];
+    auto read_block = [&](int i, int buf) {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const int r0 = (16 * i + l16) * KP + 32 * kk + 4 * g4;
+        fq[buf][kk] = concat(*reinterpret_cast<const bf16x4*>(ql + r0), *reinterpret_cast<const bf16x4*>(ql + r0 + 16));
+        if constexpr (kDelta)
+          fw[buf][kk] = concat(*reinterpret_cast<const bf16x4*>(wl + r0), *reinterpret_cast<const bf16x4*>(wl + r0 + 16));
+      }
+    };
+    read_block(0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i + 1 < 4) read_block(i + 1, (i + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);  // keep the next block's reads ahead of this block's MFMAs
+      floatx4 ax[NT], ao[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) ax[t] = ao[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          ao[t] = mfma32(sB[t][kk], fq[i & 1][kk], ao[t]);
+          if constexpr (kDelta) ax[t] = mfma32(fw[i & 1][kk], sB[t][kk], ax[t]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const bf16x4 uu = *reinterpret_cast<const bf16x4*>(utl + 16 * t * TP + 16 * i + 4 * g4);
+        floatx4 u;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) u[r] = kDelta ? f32(uu[r]) - ax[t][r] : f32(uu[r]);
+        ub[t][i] = pack4(u);
+        acc_ot[t][i] = ao[t];
+      }
+    }
+    // O_i^T += u_j^T Sc_ij^T: u_j's accumulator layout is the A layout of u_j^T; Sc_ij^T is read like Sc_ij as A
+    bf16x4 fsc[10];
+#pragma unroll
+    for (int q = 0; q < 10; ++q) fsc[q] = *reinterpret_cast<const bf16x4*>(scl + q * 256 + l16 * 16 + 4 * g4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j <= i; ++j)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc_ot[t][i] = mfma16(ub[t][j], fsc[tri_tile(i, j)], acc_ot[t][i]);
+    // S = diag(gamma) S + Kt^T u, Kt^T read transposed from the row-major tile, one tile ahead
+    bf16x8 fk[2][2];
+    auto read_kt = [&](int m, int buf) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int tok = 32 * kk + 4 * g4 + (l16 >> 2);
+        const int chn = 16 * m + 4 * (l16 & 3);
+        const int off = (s & 1) * SB + R::KT + (tok * KP + chn) * 2;
+        fk[buf][kk] = concat(lds_read_tr(smem, off), lds_read_tr(smem, off + 16 * KP * 2));
+      }
+    };
+    read_kt(0, 0);
+#pragma unroll
+    for (int m = 0; m < KT; ++m) {
+      if (m + 1 < KT) read_kt(m + 1, (m + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const float4 gm = *reinterpret_cast<const float4*>(gam + 16 * m + 4 * g4);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        st[t][m][0] *= gm.x; st[t][m][1] *= gm.y; st[t][m][2] *= gm.z; st[t][m][3] *= gm.w;
+      }
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) st[t][m] = mfma32(fk[m & 1][kk], concat(ub[t][2 * kk], ub[t][2 * kk + 1]), st[t][m]);
+    }
+    // output: lane holds O[token 16 i + l16][columns c0 + 16 t + 4 g4 .. + 3]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tk = s * kChunk + 16 * i + l16;
+      if (tk < len) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) store4(op + tk * o_st + c0 + 16 * t + 4 * g4, acc_ot[t][i], a.scale);
+      }
+    }
+    lds_barrier();
+  }
+  if (a.ht) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int m = 0; m < KT; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          a.ht[sbase + size_t(16 * m + 4 * g4 + r) * a.value_dim + c0 + 16 * t + l16] = st[t][m][r];
+  }
+}
+
+int64_t slots_per_head(const gdr_args& a) {
+  if (a.cu_seqlens) return (a.seq_len + kChunk - 1) / kChunk + a.n_seqs;
+  return int64_t(a.batch) * ((a.seq_len + kChunk - 1) / kChunk);
+}
+
+template <int VARIANT, int K, typename OutT>
+hipError_t launch_split_typed(const gdr_args& a, hipStream_t stream) {
+  const int nc = (a.seq_len + kChunk - 1) / kChunk;
+  const int64_t rec = Rec<K>::bytes(a.value_dim);
+  const int64_t n_prep = slots_per_head(a) * a.heads;
+  constexpr int prep_lds = PrepLds<K>::BYTES;
+  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::UT_SLICE);
+  static bool configured = false;  // benign race: every thread sets the same attributes
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_prep_kernel<VARIANT, K>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, prep_lds);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_scan_kernel<VARIANT, K, OutT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, scan_lds);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  if (n_prep > 0)
+    hipLaunchKernelGGL((chunk_prep_kernel<VARIANT, K>), dim3(unsigned(n_prep)), dim3(256), prep_lds, stream, a, nc,
+                       rec);
+  const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
+  const int bh = n_seq * a.heads;
+  const int n_slices = a.value_dim / kScanSlice;
+  const int xcd_map = (bh % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL((chunk_scan_kernel<VARIANT, K, OutT>), dim3(bh * n_slices), dim3(kScanThreads), scan_lds,
+                     stream, a, n_slices, xcd_map, nc, rec);
+  return hipGetLastError();
+}
+
+template <int VARIANT, int K>
+hipError_t launch_split_k(const gdr_args& a, hipStream_t stream) {
+  switch (a.out.dtype) {
+    case GDR_BF16: return launch_split_typed<VARIANT, K, __bf16>(a, stream);
+    case GDR_F16: return launch_split_typed<VARIANT, K, _Float16>(a, stream);
+    default: return launch_split_typed<VARIANT, K, float>(a, stream);
+  }
+}
+
+template <int VARIANT>
+hipError_t launch_split_v(const gdr_args& a, hipStream_t stream) {
+  return a.key_dim == 64 ? launch_split_k<VARIANT, 64>(a, stream) : launch_split_k<VARIANT, 128>(a, stream);
+}
+
+}  // namespace
+
+int64_t chunk_workspace_bytes(const gdr_args& a) {
+  const int64_t rec = a.key_dim == 64 ? Rec<64>::bytes(a.value_dim) : Rec<128>::bytes(a.value_dim);
+  return slots_per_head(a) * a.heads * rec;
+}
+
+hipError_t launch_chunk_split(const gdr_args& a, hipStream_t stream) {
+  switch (a.variant) {
+    case GDR_KDA: return launch_split_v<GDR_KDA>(a, stream);
+    case GDR_GDN: return launch_split_v<GDR_GDN>(a, stream);
+    case GDR_GLA: return launch_split_v<GDR_GLA>(a, stream);
+    default: return launch_split_v<GDR_DELTANET>(a, stream);
+  }
+}
+
+}  // namespace gdr

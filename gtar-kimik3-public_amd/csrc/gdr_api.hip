@@ -34,7 +34,8 @@ int check_view(const gdr_tensor& t, const char* name, bool required, bool f32_on
   return GDR_OK;
 }
 
-int check_common(const gdr_args* a, bool chunk) {
+// Sizes, variant, head dims and varlen fields: everything that shapes the work, no pointer dereferenced.
+int check_shape(const gdr_args* a, bool chunk) {
   if (!a) return fail(GDR_ERR_INVALID, "args is NULL");
   if (a->abi_version != GDR_ABI_VERSION)
     return fail(GDR_ERR_INVALID, "abi_version %d, library implements %d", a->abi_version, GDR_ABI_VERSION);
@@ -48,9 +49,19 @@ int check_common(const gdr_args* a, bool chunk) {
   if (a->value_dim < vmul || a->value_dim % vmul != 0 || a->value_dim > 1024)
     return fail(GDR_ERR_UNSUPPORTED, "value dim %d not supported (a multiple of %d up to 1024)", a->value_dim,
                 vmul);
+  if (a->cu_seqlens) {
+    if (!chunk) return fail(GDR_ERR_INVALID, "cu_seqlens is only accepted by the chunk mode");
+    if (a->batch != 1) return fail(GDR_ERR_INVALID, "cu_seqlens requires batch == 1 (got %d)", a->batch);
+    if (a->n_seqs < 1) return fail(GDR_ERR_INVALID, "cu_seqlens given with n_seqs=%d", a->n_seqs);
+  }
+  return GDR_OK;
+}
+
+int check_common(const gdr_args* a, bool chunk) {
+  int rc = check_shape(a, chunk);
+  if (rc) return rc;
   const bool has_gate = a->variant != GDR_DELTANET;
   const bool has_beta = a->variant != GDR_GLA;
-  int rc;
   if ((rc = check_view(a->q, "query", true, false))) return rc;
   if ((rc = check_view(a->k, "key", true, false))) return rc;
   if ((rc = check_view(a->v, "value", true, false))) return rc;
@@ -61,11 +72,6 @@ int check_common(const gdr_args* a, bool chunk) {
   if (!has_beta && a->beta.ptr) return fail(GDR_ERR_INVALID, "GLA takes no beta");
   if ((reinterpret_cast<uintptr_t>(a->h0) | reinterpret_cast<uintptr_t>(a->ht)) % 16 != 0)
     return fail(GDR_ERR_INVALID, "initial/final state must be 16-byte aligned");
-  if (a->cu_seqlens) {
-    if (!chunk) return fail(GDR_ERR_INVALID, "cu_seqlens is only accepted by the chunk mode");
-    if (a->batch != 1) return fail(GDR_ERR_INVALID, "cu_seqlens requires batch == 1 (got %d)", a->batch);
-    if (a->n_seqs < 1) return fail(GDR_ERR_INVALID, "cu_seqlens given with n_seqs=%d", a->n_seqs);
-  }
   return GDR_OK;
 }
 
@@ -89,6 +95,13 @@ int gdr_recurrent_fwd(const gdr_args* a, hipStream_t stream) {
   return GDR_OK;
 }
 
+int64_t gdr_chunk_workspace_bytes(const gdr_args* a) {
+  const int rc = check_shape(a, true);
+  if (rc) return rc;
+  g_last_error.clear();
+  return gdr::chunk_workspace_bytes(*a);
+}
+
 int gdr_chunk_fwd(const gdr_args* a, hipStream_t stream) {
   int rc = check_common(a, true);
   if (rc) return rc;
@@ -107,7 +120,18 @@ int gdr_chunk_fwd(const gdr_args* a, hipStream_t stream) {
         (t.stride_t * es) % 16)
       return fail(GDR_ERR_INVALID, "%s: base pointer and b/h/t strides must be 16-byte aligned", names[i]);
   }
-  hipError_t e = gdr::launch_chunk(*a, stream);
+  const int64_t need = gdr::chunk_workspace_bytes(*a);
+  hipError_t e;
+  if (a->workspace) {
+    if (a->workspace_bytes < need)
+      return fail(GDR_ERR_INVALID, "workspace of %lld bytes given, %lld required", (long long)a->workspace_bytes,
+                  (long long)need);
+    if (reinterpret_cast<uintptr_t>(a->workspace) % 256)
+      return fail(GDR_ERR_INVALID, "workspace must be 256-byte aligned");
+    e = gdr::launch_chunk_split(*a, stream);
+  } else {
+    e = gdr::launch_chunk(*a, stream);
+  }
   if (e != hipSuccess) return fail(GDR_ERR_HIP, "chunk launch failed: %s", hipGetErrorString(e));
   g_last_error.clear();
   return GDR_OK;

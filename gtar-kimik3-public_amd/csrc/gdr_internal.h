@@ -13,4 +13,9 @@ hipError_t launch_recurrent(const gdr_args& a, hipStream_t stream);
 // Enqueue the chunkwise forward; `a` has been validated (q, k, v share one dtype).
 hipError_t launch_chunk(const gdr_args& a, hipStream_t stream);
 
+// Chunkwise forward as a chunk-parallel preparation launch plus a state-scan launch over a workspace of
+// chunk_workspace_bytes(a) bytes at a.workspace.
+int64_t chunk_workspace_bytes(const gdr_args& a);
+hipError_t launch_chunk_split(const gdr_args& a, hipStream_t stream);
+
 }  // namespace gdr

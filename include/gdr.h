@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GDR_ABI_VERSION 1
+#define GDR_ABI_VERSION 2
 
 typedef enum gdr_variant { GDR_KDA = 0, GDR_GDN = 1, GDR_GLA = 2, GDR_DELTANET = 3 } gdr_variant;
 
@@ -72,6 +72,9 @@ typedef struct gdr_args {
   const int32_t* cu_seqlens; /* device int32 [n_seqs + 1] packed-sequence offsets, or NULL */
   int32_t n_seqs;            /* number of packed sequences (N); ignored when cu_seqlens is NULL (N = B) */
   int32_t reserved;
+  void* workspace;           /* chunk mode: device scratch of gdr_chunk_workspace_bytes(args) bytes, 256-aligned;
+                                NULL selects the single-launch fused kernel, which needs none (and is slower) */
+  int64_t workspace_bytes;   /* size of `workspace` */
 } gdr_args;
 
 /* Chunkwise forward (prefill).  Replaces, for all four variants, the forward of
@@ -84,6 +87,13 @@ typedef struct gdr_args {
  * operand type; the Python layer casts); out may be bf16, f16 or f32.
  * Supports K in {64, 128}, V a multiple of 64, any T >= 1, and packed varlen input through cu_seqlens. */
 int gdr_chunk_fwd(const gdr_args* args, hipStream_t stream);
+
+/* Bytes of device workspace gdr_chunk_fwd needs for `args` (sizes, variant, key/value dims and varlen fields are
+ * read; no pointer is dereferenced), or a negative gdr_status.  The workspace holds one record per (chunk, head)
+ * that the chunk-parallel preparation kernel writes and the state-scan kernel reads: the reference keeps the
+ * same kind of intermediates (gate cumsum, P, A, W, U, States) in tensors it allocates per call
+ * (src/ops/kimi_delta_attention.py:540-553).  For B=4, T=4096, H=16, K=V=128 it is 317 MB. */
+int64_t gdr_chunk_workspace_bytes(const gdr_args* args);
 
 /* Recurrent forward (decode).  Replaces the `_recurrent_forward` Triton launch of
  *   recurrent_kimi_delta_attention     src/ops/kimi_delta_attention.py:666-692 (kernel :38-68)

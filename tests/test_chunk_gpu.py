@@ -8,6 +8,8 @@ elementwise path), correlated keys, random initial states, plus the benchmark sh
 layout, packed varlen input and state passing.
 """
 
+import importlib
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -141,3 +143,22 @@ def test_chunk_variant_sweep_full_size(variant):
     print(f"chunk {variant} B=2 T=8192 H=16 K=V=128", flush=True)
     inp = workloads.make_inputs(variant, 2, 8192, 16, 128, 128, seed=0, device="cuda")
     _check(variant, inp, f"chunk {variant} full size")
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_chunk_without_workspace_matches_oracle(variant):
+    """workspace = NULL selects the single-launch kernel that needs no scratch memory."""
+    lib = importlib.import_module("gtar-kimik3-public_amd._lib")
+    B, H, T, K, V = 2, 2, 200, 128, 128
+    inp = workloads.make_inputs(variant, B, T, H, K, V, seed=3, state_std=0.5, device="cuda")
+    out = torch.empty(B, H, T, V, dtype=torch.bfloat16, device="cuda")
+    ht = torch.empty(B, H, K, V, dtype=torch.float32, device="cuda")
+    vid = {"kda": lib.KDA, "gdn": lib.GDN, "gla": lib.GLA, "deltanet": lib.DELTANET}[variant]
+    args = lib.make_args(vid, inp.query, inp.key, inp.value, inp.gate, inp.beta, out, K ** -0.5, inp.initial_state,
+                         ht)
+    assert not args.workspace
+    lib.launch("gdr_chunk_fwd", args, out.device)
+    torch.cuda.synchronize()
+    q, k, v, g, beta, h0 = oracle_args(inp)
+    ref_o, ref_s = oracle.chunkwise(variant, q, k, v, g, beta, None, h0)
+    assert out_error(out, ref_o) <= OUT_TOL and state_error(ht, ref_s) <= STATE_TOL
