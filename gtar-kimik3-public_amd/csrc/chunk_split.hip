@@ -59,29 +59,44 @@ template <int K>
 struct PrepLds {
   static constexpr int KP = K + 8;
   static constexpr int KAP = 0;                   // bf16 [64][KP] k e^{a_p - b}  (block-end anchor, strip keys)
-  static constexpr int AINV = KAP;                // bf16 [4][256] (I + diag(beta) P_ii)^{-1}, after the strips
+  static constexpr int VST = KAP;                 //   after the strips: bf16 [64][KP] one K-column pass of V
   static constexpr int KD = KAP + 64 * KP * 2;    // bf16 [64][KP] k e^B         (right-hand side of the solve)
   static constexpr int SC = KD + 64 * KP * 2;     // bf16 [10][256] gated score tiles
+  static constexpr int EPRE = SC;                 //   before the strips: fp32 [4][K] e^{a_{i-1}} per block
+  static constexpr int ETAIL = SC + 4 * K * 4;    //   before the strips: fp32 [4][K] e^{B_end - a_i} per block
   static constexpr int NEGL = SC + 10 * 512;      // bf16 [6][256]  -diag(beta) P, tile (i, j < i)
   static constexpr int LII = NEGL + 6 * 512;      // fp32 [4][256]  diag(beta) P_ii (strictly lower)
   static constexpr int TOT = LII + 4 * 1024;      // fp32 [4][K]    per-block log2-gate totals
+  static constexpr int AINV = TOT;                //   after the strips: bf16 [4][256] (I + diag(beta) P_ii)^{-1}
   static constexpr int RDS = TOT + 4 * K * 4;     // fp32 [4][K]    diagonal key factor e^{-T_i} (0: hot channel)
   static constexpr int FAR = RDS + 4 * K * 4;     // fp32 [3][K]    key factors of tiles (2,0), (3,0), (3,1)
   static constexpr int BETA = FAR + 3 * K * 4;    // fp32 [64]
   static constexpr int BYTES = BETA + 256;
+  static_assert(8 * K * 4 <= 16 * 512, "EPRE/ETAIL alias");
+  static_assert(4 * 512 <= 11 * K * 4, "AINV alias");
 };
 
-// Four consecutive outputs (scaled) in one 8-byte (16-bit types) or 16-byte (fp32) store.
-__device__ __forceinline__ void store4(__bf16* dst, floatx4 v, float s) {
-  *reinterpret_cast<bf16x4*>(dst) = bf16x4{bf(v[0] * s), bf(v[1] * s), bf(v[2] * s), bf(v[3] * s)};
+// Inclusive prefix sum over the 16 lanes of each DPP row (v_add_f32 with row_shr:1, 2, 4, 8; lanes shifted in from
+// outside the row contribute 0).
+__device__ __forceinline__ float row_scan16(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, true));
+  return x;
 }
-__device__ __forceinline__ void store4(_Float16* dst, floatx4 v, float s) {
+
+// Four consecutive outputs in one 8-byte (16-bit types) or 16-byte (fp32) store.
+__device__ __forceinline__ void store4(__bf16* dst, floatx4 v) {
+  *reinterpret_cast<bf16x4*>(dst) = bf16x4{bf(v[0]), bf(v[1]), bf(v[2]), bf(v[3])};
+}
+__device__ __forceinline__ void store4(_Float16* dst, floatx4 v) {
   typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4;
-  *reinterpret_cast<f16x4*>(dst) = f16x4{static_cast<_Float16>(v[0] * s), static_cast<_Float16>(v[1] * s),
-                                         static_cast<_Float16>(v[2] * s), static_cast<_Float16>(v[3] * s)};
+  *reinterpret_cast<f16x4*>(dst) = f16x4{static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]),
+                                         static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
 }
-__device__ __forceinline__ void store4(float* dst, floatx4 v, float s) {
-  *reinterpret_cast<float4*>(dst) = make_float4(v[0] * s, v[1] * s, v[2] * s, v[3] * s);
+__device__ __forceinline__ void store4(float* dst, floatx4 v) {
+  *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
 // First workspace slot of packed sequence n: floor(bos / 64) + n.  Slots of consecutive sequences never
@@ -138,9 +153,12 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
   unsigned char* rec = static_cast<unsigned char*>(a.workspace) + (int64_t(slot) * H + h) * rec_bytes;
 
   __bf16* kap = reinterpret_cast<__bf16*>(smem + L::KAP);
+  __bf16* vst = reinterpret_cast<__bf16*>(smem + L::VST);
   __bf16* ainv = reinterpret_cast<__bf16*>(smem + L::AINV);
   __bf16* kd = reinterpret_cast<__bf16*>(smem + L::KD);
   __bf16* sct = reinterpret_cast<__bf16*>(smem + L::SC);
+  float* epre_v = reinterpret_cast<float*>(smem + L::EPRE);
+  float* etail_v = reinterpret_cast<float*>(smem + L::ETAIL);
   __bf16* negl = reinterpret_cast<__bf16*>(smem + L::NEGL);
   float* lii = reinterpret_cast<float*>(smem + L::LII);
   float* tot = reinterpret_cast<float*>(smem + L::TOT);
@@ -155,7 +173,37 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
   const bool valid = crow < len;
   const int tc = min(crow, len - 1);
 
-  // ---- 1. loads: this lane's q, k, gate, beta row; the value rows of the wave's first U tile ----
+  // V is consumed in passes of K columns staged row-major in LDS (the strip-key region, free by then).
+  constexpr int kVPieces = 64 * K / 8;                 // 16-byte pieces of a full pass
+  constexpr int kVLoads = (kVPieces + 255) / 256;      // per thread
+  const int n_pass = (a.value_dim + K - 1) / K;
+  auto pass_width = [&](int pass) { return min(K, a.value_dim - pass * K); };
+  uint4 vpre[kVLoads];
+  auto load_v_pass = [&](int pass) {  // unconditional loads from clamped rows / pieces; masked when staged
+    const int w8 = pass_width(pass) / 8;
+#pragma unroll
+    for (int i = 0; i < kVLoads; ++i) {
+      const int pc = min(int(threadIdx.x) + 256 * i, 64 * w8 - 1);
+      const int row = pc / w8, cc = (pc % w8) * 8;
+      const int t = min(c * kChunk + row, len - 1);
+      vpre[i] = *reinterpret_cast<const uint4*>(x.vp + t * x.v_st + pass * K + cc);
+    }
+  };
+  auto stage_v_pass = [&](int pass) {
+    const int w8 = pass_width(pass) / 8;
+#pragma unroll
+    for (int i = 0; i < kVLoads; ++i) {
+      const int pc = threadIdx.x + 256 * i;
+      if (pc < 64 * w8) {
+        const int row = pc / w8, cc = (pc % w8) * 8;
+        const uint32_t keep = c * kChunk + row < len ? 0xffffffffu : 0u;
+        *reinterpret_cast<uint4*>(vst + row * KP + cc) =
+            make_uint4(vpre[i].x & keep, vpre[i].y & keep, vpre[i].z & keep, vpre[i].w & keep);
+      }
+    }
+  };
+
+  // ---- 1. loads: this lane's q, k, gate, beta row; the first pass of V ----
   uint4 qraw[KS], kraw[KS];
   float bl[KS][8];
 #pragma unroll
@@ -184,47 +232,15 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
       for (int j = 0; j < 8; ++j) bl[kk][j] = 0.f;
   }
   const float beta_t = kDelta ? x.betap[tc * x.b_st] : 0.f;
+  load_v_pass(0);
 
-  const int kt_tiles = kDelta ? K / 16 : 0, n_tiles = kt_tiles + a.value_dim / 16;
-  // Value rows of the wave's next U tile (D layout: rows 16 i + 4 g4 + r, column col), fetched one tile ahead so
-  // a global load is never waited on right after it is issued.
-  uint32_t vnext[4][4];
-  auto fetch_v = [&](int nt) {
-    const int col = 16 * (nt - kt_tiles) + l16;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = min(c * kChunk + 16 * i + 4 * g4 + r, len - 1);
-        vnext[i][r] = reinterpret_cast<const uint16_t*>(x.vp)[t * x.v_st + col];
-      }
-  };
-  int first_u = wave;
-  while (first_u < kt_tiles) first_u += 4;
-  if (first_u < n_tiles) fetch_v(first_u);
-
-  // ---- 2. in-block inclusive cumsum of the log2 gate over the 16 rows (lanes l16); block totals ----
-  float tw[KS][8];
+  // ---- 2. in-block inclusive cumsum of the log2 gate over the 16 rows (one DPP row per channel group) ----
   if constexpr (kGate) {
     const float keep = valid ? kLog2e : 0.f;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) bl[kk][j] *= keep;
-#pragma unroll
-    for (int off = 1; off < 16; off *= 2) {
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float y = __shfl_up(bl[kk][j], off, 16);
-          if (l16 >= off) bl[kk][j] += y;
-        }
-    }
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) tw[kk][j] = __shfl(bl[kk][j], 15, 16);
+      for (int j = 0; j < 8; ++j) bl[kk][j] = row_scan16(bl[kk][j] * keep);
     if (l16 == 15) {
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
@@ -233,30 +249,40 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
         *reinterpret_cast<float4*>(dst + 4) = make_float4(bl[kk][4], bl[kk][5], bl[kk][6], bl[kk][7]);
       }
     }
-  } else {
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) tw[kk][j] = 0.f;
   }
   if (g4 == 0) sbeta[16 * p + l16] = valid ? beta_t : 0.f;
   lds_barrier();
 
-  // ---- 3a. key factors of the strips, spread over the workgroup: RDS[i] = e^{-T_i} (0 for a hot channel),
-  // FAR = e^{a_{i-1} - a_j} for the far tiles (2,0), (3,0), (3,1) ----
+  // ---- 3a. channel vectors, spread over the workgroup: EPRE[i] = e^{a_{i-1}}, ETAIL[i] = e^{B_end - a_i};
+  // strip key factors RDS[i] = e^{-T_i} (0 for a hot channel) and FAR = e^{a_{i-1} - a_j} for tiles (2,0),
+  // (3,0), (3,1) ----
   if constexpr (kGate) {
-    for (int idx = threadIdx.x; idx < 7 * K; idx += 256) {
+    for (int idx = threadIdx.x; idx < 15 * K; idx += 256) {
       const int v = idx / K, ch = idx % K;
+      const float t0 = tot[ch], t1 = tot[K + ch], t2 = tot[2 * K + ch], t3 = tot[3 * K + ch];
       if (v < 4) {
-        const float t = tot[v * K + ch];
+        const float t = v == 0 ? t0 : v == 1 ? t1 : v == 2 ? t2 : t3;
         rds[v * K + ch] = -t > kHot ? 0.f : __builtin_amdgcn_exp2f(-t);
+      } else if (v < 7) {
+        far[(v - 4) * K + ch] = __builtin_amdgcn_exp2f(v == 4 ? t1 : (v == 5 ? t1 + t2 : t2));
+      } else if (v < 11) {
+        const int i = v - 7;
+        epre_v[i * K + ch] = __builtin_amdgcn_exp2f(i == 0 ? 0.f : i == 1 ? t0 : i == 2 ? t0 + t1 : t0 + t1 + t2);
       } else {
-        const float e = v == 4 ? tot[K + ch] : (v == 5 ? tot[K + ch] + tot[2 * K + ch] : tot[2 * K + ch]);
-        far[(v - 4) * K + ch] = __builtin_amdgcn_exp2f(e);
+        const int i = v - 11;
+        etail_v[i * K + ch] = __builtin_amdgcn_exp2f(i == 0 ? t1 + t2 + t3 : i == 1 ? t2 + t3 : i == 2 ? t3 : 0.f);
       }
     }
   }
-  // ---- 3b. operands.  Block anchors a_{p-1} (pre) and a_p = a_{p-1} + T_p; chunk-end tail = B_end - a_p ----
+  if (threadIdx.x < K) {
+    const int ch = threadIdx.x;
+    const float b_end = kGate ? tot[ch] + tot[K + ch] + tot[2 * K + ch] + tot[3 * K + ch] : 0.f;
+    reinterpret_cast<float*>(rec + R::GAM)[ch] = kGate ? __builtin_amdgcn_exp2f(b_end) : 1.f;
+  }
+  lds_barrier();
+
+  // ---- 3b. operands: Lq, Lk = (q, k) e^{B - a_{p-1}} (block-start anchor), Kap = k e^{a_p - B} (block-end
+  // anchor); Q e^B (times the output scale) and K e^{B_end - B} to the record ----
   bf16x8 lq[KS], lk[KS];
   const uint32_t keep_bits = valid ? 0xffffffffu : 0u;
 #pragma unroll
@@ -267,47 +293,44 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
                        qraw[kk].w & keep_bits), qf);
     unpack8(make_uint4(kraw[kk].x & keep_bits, kraw[kk].y & keep_bits, kraw[kk].z & keep_bits,
                        kraw[kk].w & keep_bits), kf);
-    float pre[8], tail[8];
+    float tw[8], ep[8], et[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) pre[j] = tail[j] = 0.f;
+    for (int j = 0; j < 8; ++j) tw[j] = 0.f, ep[j] = et[j] = 1.f;
     if constexpr (kGate) {
+      const float4 a0 = *reinterpret_cast<const float4*>(tot + p * K + ch);
+      const float4 a1 = *reinterpret_cast<const float4*>(tot + p * K + ch + 4);
+      const float4 b0 = *reinterpret_cast<const float4*>(epre_v + p * K + ch);
+      const float4 b1 = *reinterpret_cast<const float4*>(epre_v + p * K + ch + 4);
+      const float4 d0 = *reinterpret_cast<const float4*>(etail_v + p * K + ch);
+      const float4 d1 = *reinterpret_cast<const float4*>(etail_v + p * K + ch + 4);
+      const float ta[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      const float tb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+      const float td[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        if (m == p) continue;
-        const float4 t0 = *reinterpret_cast<const float4*>(tot + m * K + ch);
-        const float4 t1 = *reinterpret_cast<const float4*>(tot + m * K + ch + 4);
-        const float tv[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (m < p) pre[j] += tv[j];
-          else tail[j] += tv[j];
-        }
-      }
+      for (int j = 0; j < 8; ++j) tw[j] = ta[j], ep[j] = tb[j], et[j] = td[j];
     }
     bf16x8 vq, vk, vkap, vkd, vkt, vqd;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      float ell = 1.f, rho = 1.f, epre = 1.f, etail = 1.f;
+      float ell = 1.f, rho = 1.f;
       if constexpr (kGate) {
         ell = __builtin_amdgcn_exp2f(bl[kk][j]);
-        rho = __builtin_amdgcn_exp2f(tw[kk][j] - bl[kk][j]);
-        epre = __builtin_amdgcn_exp2f(pre[j]);
-        etail = __builtin_amdgcn_exp2f(tail[j]);
+        rho = __builtin_amdgcn_exp2f(tw[j] - bl[kk][j]);
       }
       const float q1 = qf[j] * ell, k1 = kf[j] * ell, kp1 = kf[j] * rho;
       vq[j] = bf(q1);
       vk[j] = bf(k1);
       vkap[j] = bf(kp1);
-      vkd[j] = bf(k1 * epre);
-      vkt[j] = bf(kp1 * etail);
-      vqd[j] = bf(q1 * epre);
+      vkd[j] = bf(k1 * ep[j]);
+      vkt[j] = bf(kp1 * et[j]);
+      vqd[j] = bf(q1 * (ep[j] * a.scale));
     }
     lq[kk] = vq;
     lk[kk] = vk;
     const int ro = (16 * p + l16) * KP + ch;
     *reinterpret_cast<bf16x8*>(kap + ro) = vkap;
     if constexpr (kDelta) *reinterpret_cast<bf16x8*>(kd + ro) = vkd;
-    *reinterpret_cast<bf16x8*>(rec + R::QD + ro * 2) = vqd;  // Q e^B
+    *reinterpret_cast<bf16x8*>(rec + R::QD + ro * 2) = vqd;  // scale Q e^B
     *reinterpret_cast<bf16x8*>(rec + R::KT + ro * 2) = vkt;  // K e^{B_end - B}
   }
   lds_barrier();
@@ -360,7 +383,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
   }
   lds_barrier();
 
-  // ---- 5. diagonal inverses (wave p, 16 lanes, fp32 forward substitution); score tiles and e^{B_end} out ----
+  // ---- 5. diagonal inverses (wave p, 16 lanes, fp32 forward substitution); V pass 0 staged; score tiles
+  // (times the output scale) to the record ----
   if constexpr (kDelta) {
     if (lane < 16) {
       const float* lt = lii + p * 256;
@@ -386,49 +410,32 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
       for (int r = 0; r < 16; ++r) ainv[p * 256 + r * 16 + lane] = bf(xcol[r]);
     }
   }
-  for (int i = threadIdx.x; i < 10 * 256 * 2 / 16; i += 256)
-    reinterpret_cast<uint4*>(rec + R::SC)[i] = reinterpret_cast<const uint4*>(sct)[i];
-  if (threadIdx.x < K) {
-    float b_end = 0.f;
-    if constexpr (kGate)
-      b_end = tot[threadIdx.x] + tot[K + threadIdx.x] + tot[2 * K + threadIdx.x] + tot[3 * K + threadIdx.x];
-    reinterpret_cast<float*>(rec + R::GAM)[threadIdx.x] = kGate ? __builtin_amdgcn_exp2f(b_end) : 1.f;
+  stage_v_pass(0);
+  for (int i = threadIdx.x; i < 10 * 256 / 8; i += 256) {
+    bf16x8 v8 = reinterpret_cast<const bf16x8*>(sct)[i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v8[e] = bf(f32(v8[e]) * a.scale);
+    reinterpret_cast<bf16x8*>(rec + R::SC)[i] = v8;
   }
   lds_barrier();
 
-  // ---- 6. [W | U] = A diag(beta) [K e^B | V] by blocked forward substitution; wave w owns N-tiles w, w+4, ...
+  // ---- 6. [W | U] = A diag(beta) [K e^B | V] by blocked forward substitution over 16-column tiles.
   // Block i: Y_i = diag(beta_i) R_i - sum_{j<i} L_ij X_j,  X_i = A_ii Y_i.  X_i (accumulator layout: rows 4 g4 + r,
   // column l16) feeds the later blocks; for W the transposed product X_i^T = Y_i^T A_ii^T (the same two operands
-  // with their roles swapped) puts four consecutive channels of one row in each lane for 8-byte row stores. ----
+  // with their roles swapped) puts four consecutive channels of one row in each lane for 8-byte row stores.  The
+  // right-hand side comes from row-major LDS tiles through one transposing read per block. ----
   __bf16* wrec = reinterpret_cast<__bf16*>(rec + R::W);
   __bf16* utrec = reinterpret_cast<__bf16*>(rec + R::FIX);
   const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  for (int nt = wave; nt < n_tiles; nt += 4) {
-    const bool is_w = nt < kt_tiles;
-    const int col0 = 16 * (is_w ? nt : nt - kt_tiles);
-    float vcur[4][4];
-    if (!is_w) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          vcur[i][r] = c * kChunk + 16 * i + 4 * g4 + r < len ? bf16_bits_to_f32(uint16_t(vnext[i][r])) : 0.f;
-      if (nt + 4 < n_tiles) fetch_v(nt + 4);
-    }
+  auto solve_tile = [&](int rhs_off, int col0, bool is_w, int out_col0) {
     bf16x4 xs[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      const int off = rhs_off + ((16 * i + 4 * g4 + (l16 >> 2)) * KP + col0 + 4 * (l16 & 3)) * 2;
+      const bf16x4 rv = lds_read_tr(smem, off);  // rows 16 i + 4 g4 + r, column col0 + l16
       floatx4 z;
-      if (is_w) {
-        // K e^B rows 16 i + 4 g4 + r, column col0 + l16, with one transposing read
-        const int off = L::KD + ((16 * i + 4 * g4 + (l16 >> 2)) * KP + col0 + 4 * (l16 & 3)) * 2;
-        const bf16x4 kv = lds_read_tr(smem, off);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) z[r] = f32(kv[r]);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) z[r] = vcur[i][r];
-      }
+      for (int r = 0; r < 4; ++r) z[r] = f32(rv[r]);
       if constexpr (kDelta) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) z[r] *= sbeta[16 * i + 4 * g4 + r];
@@ -441,14 +448,27 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
         const bf16x4 zb = pack4(z);
         xs[i] = pack4(mfma16(ai, zb, zero4));
         if (is_w) {
-          const bf16x4 xt = pack4(mfma16(zb, ai, zero4));  // X_i^T: row 16 i + l16, channels col0 + 4 g4 + r
-          *reinterpret_cast<bf16x4*>(wrec + (16 * i + l16) * KP + col0 + 4 * g4) = xt;
+          const bf16x4 xt = pack4(mfma16(zb, ai, zero4));  // X_i^T: row 16 i + l16, channels out_col0 + 4 g4 + r
+          *reinterpret_cast<bf16x4*>(wrec + (16 * i + l16) * KP + out_col0 + 4 * g4) = xt;
         }
       } else {
         xs[i] = pack4(z);
       }
-      if (!is_w) *reinterpret_cast<bf16x4*>(utrec + (col0 + l16) * TP + 16 * i + 4 * g4) = xs[i];
+      if (!is_w) *reinterpret_cast<bf16x4*>(utrec + (out_col0 + l16) * TP + 16 * i + 4 * g4) = xs[i];
     }
+  };
+  if constexpr (kDelta) {
+    for (int nt = wave; nt < K / 16; nt += 4) solve_tile(L::KD, 16 * nt, true, 16 * nt);
+  }
+  for (int pass = 0; pass < n_pass; ++pass) {
+    if (pass > 0) {  // value dims beyond K: later passes staged synchronously
+      load_v_pass(pass);
+      lds_barrier();
+      stage_v_pass(pass);
+      lds_barrier();
+    }
+    const int tiles = pass_width(pass) / 16;
+    for (int nt = wave; nt < tiles; nt += 4) solve_tile(L::VST, 16 * nt, false, pass * K + 16 * nt);
   }
 }
 
@@ -643,7 +663,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
       const int tk = s * kChunk + 16 * i + l16;
       if (tk < len) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) store4(op + tk * o_st + c0 + 16 * t + 4 * g4, acc_ot[t][i], a.scale);
+        for (int t = 0; t < NT; ++t) store4(op + tk * o_st + c0 + 16 * t + 4 * g4, acc_ot[t][i]);
       }
     }
     lds_barrier();
