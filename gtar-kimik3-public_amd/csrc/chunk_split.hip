@@ -42,12 +42,17 @@ constexpr int kScanSlice = 64;  // value columns per scan workgroup
 // Workspace record of one (chunk, head); byte offsets.  UT (U^T, [V][TP]) closes the record.
 template <int K>
 struct Rec {
-  static constexpr int KP = K + 8;   // row pitch of [64][K] bf16 arrays (16-byte skew per row)
-  static constexpr int TP = 64 + 8;  // row pitch of [*][64 tokens] bf16 arrays
-  static constexpr int W = 0;                                   // bf16 [64][KP]  A diag(beta) K e^B
-  static constexpr int QD = W + 64 * KP * 2;                    // bf16 [64][KP]  Q e^B
-  static constexpr int KT = QD + 64 * KP * 2;                   // bf16 [64][KP]  K e^{B_end - B}
-  static constexpr int SC = KT + 64 * KP * 2;                   // bf16 [10][16][16] gated scores, tile (i, j <= i)
+  // W and Q e^B are A operands of 16x16x32 MFMAs whose B operand is the state in the two-tile k order: within
+  // each 32-channel group, stored position 8 g + j holds channel 4 g + j (j < 4) or 16 + 4 g + j - 4 (j >= 4), so
+  // every lane reads its 8 operands with one 16-byte LDS read.  K e^{B_end - B} is read with the transposing LDS
+  // read, which is conflict-free at a row pitch of 8 (mod 64) dwords.
+  static constexpr int KP = K + 8;    // row pitch of W and Q e^B (bf16)
+  static constexpr int KTP = K + 16;  // row pitch of K e^{B_end - B} (bf16)
+  static constexpr int TP = 64 + 8;   // row pitch of [*][64 tokens] bf16 arrays
+  static constexpr int W = 0;                                   // bf16 [64][KP]  A diag(beta) K e^B (permuted)
+  static constexpr int QD = W + 64 * KP * 2;                    // bf16 [64][KP]  scale Q e^B (permuted)
+  static constexpr int KT = QD + 64 * KP * 2;                   // bf16 [64][KTP] K e^{B_end - B}
+  static constexpr int SC = KT + 64 * KTP * 2;                  // bf16 [10][16][16] gated scores, tile (i, j <= i)
   static constexpr int GAM = SC + 10 * 256 * 2;                 // fp32 [K] e^{B_end}
   static constexpr int FIX = ((GAM + K * 4 + 255) / 256) * 256;  // start of UT
   static constexpr int UT_SLICE = kScanSlice * TP * 2;          // bytes of 64 rows of UT
@@ -330,8 +335,13 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
     const int ro = (16 * p + l16) * KP + ch;
     *reinterpret_cast<bf16x8*>(kap + ro) = vkap;
     if constexpr (kDelta) *reinterpret_cast<bf16x8*>(kd + ro) = vkd;
-    *reinterpret_cast<bf16x8*>(rec + R::QD + ro * 2) = vqd;  // scale Q e^B
-    *reinterpret_cast<bf16x8*>(rec + R::KT + ro * 2) = vkt;  // K e^{B_end - B}
+    // scale Q e^B in the permuted channel order: this lane's channels 8 g4 .. 8 g4 + 7 of the group land as two
+    // 4-channel pieces at positions pb and pb + 8
+    const int pb = (16 * p + l16) * R::KP + 32 * kk + 16 * (g4 & 1) + 4 * (g4 >> 1);
+    __bf16* qrec = reinterpret_cast<__bf16*>(rec + R::QD);
+    *reinterpret_cast<bf16x4*>(qrec + pb) = bf16x4{vqd[0], vqd[1], vqd[2], vqd[3]};
+    *reinterpret_cast<bf16x4*>(qrec + pb + 8) = bf16x4{vqd[4], vqd[5], vqd[6], vqd[7]};
+    *reinterpret_cast<bf16x8*>(rec + R::KT + ((16 * p + l16) * R::KTP + ch) * 2) = vkt;  // K e^{B_end - B}
   }
   lds_barrier();
 
@@ -448,8 +458,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
         const bf16x4 zb = pack4(z);
         xs[i] = pack4(mfma16(ai, zb, zero4));
         if (is_w) {
-          const bf16x4 xt = pack4(mfma16(zb, ai, zero4));  // X_i^T: row 16 i + l16, channels out_col0 + 4 g4 + r
-          *reinterpret_cast<bf16x4*>(wrec + (16 * i + l16) * KP + out_col0 + 4 * g4) = xt;
+          // X_i^T: row 16 i + l16, channels out_col0 + 4 g4 + r, stored in the permuted channel order
+          const bf16x4 xt = pack4(mfma16(zb, ai, zero4));
+          const int wpos = 32 * (out_col0 >> 5) + 8 * g4 + 4 * ((out_col0 >> 4) & 1);
+          *reinterpret_cast<bf16x4*>(wrec + (16 * i + l16) * R::KP + wpos) = xt;
         }
       } else {
         xs[i] = pack4(z);
@@ -475,7 +487,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
 // =============================== scan: one workgroup per (sequence, head) x 64 columns ===============================
 constexpr int kScanTiles = 1;                          // 16-column tiles per compute wave
 constexpr int kScanCompute = kScanSlice / (16 * kScanTiles);  // compute waves per scan workgroup
-constexpr int kScanLoaders = 2;                        // loader waves per scan workgroup
+constexpr int kScanLoaders = 4;                        // loader waves per scan workgroup
 constexpr int kScanThreads = 64 * (kScanCompute + kScanLoaders);
 
 template <int VARIANT, int K, typename OutT>
@@ -512,7 +524,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
   const int nchunks = (len + kChunk - 1) / kChunk;
   const int v0 = slice * kScanSlice;
   const unsigned char* ws = static_cast<const unsigned char*>(a.workspace);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // wave index made explicitly wave-uniform so that role and group branches are scalar branches
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
 
   if (wave >= kScanCompute) {
     // ---------------- loader waves ----------------
@@ -589,10 +602,9 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
     auto read_block = [&](int i, int buf) {
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
-        const int r0 = (16 * i + l16) * KP + 32 * kk + 4 * g4;
-        fq[buf][kk] = concat(*reinterpret_cast<const bf16x4*>(ql + r0), *reinterpret_cast<const bf16x4*>(ql + r0 + 16));
-        if constexpr (kDelta)
-          fw[buf][kk] = concat(*reinterpret_cast<const bf16x4*>(wl + r0), *reinterpret_cast<const bf16x4*>(wl + r0 + 16));
+        const int r0 = (16 * i + l16) * KP + 32 * kk + 8 * g4;  // permuted order: one 16-byte read
+        fq[buf][kk] = *reinterpret_cast<const bf16x8*>(ql + r0);
+        if constexpr (kDelta) fw[buf][kk] = *reinterpret_cast<const bf16x8*>(wl + r0);
       }
     };
     read_block(0, 0);
@@ -638,8 +650,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
       for (int kk = 0; kk < 2; ++kk) {
         const int tok = 32 * kk + 4 * g4 + (l16 >> 2);
         const int chn = 16 * m + 4 * (l16 & 3);
-        const int off = (s & 1) * SB + R::KT + (tok * KP + chn) * 2;
-        fk[buf][kk] = concat(lds_read_tr(smem, off), lds_read_tr(smem, off + 16 * KP * 2));
+        const int off = (s & 1) * SB + R::KT + (tok * R::KTP + chn) * 2;
+        fk[buf][kk] = concat(lds_read_tr(smem, off), lds_read_tr(smem, off + 16 * R::KTP * 2));
       }
     };
     read_kt(0, 0);
