@@ -3,11 +3,12 @@
 One JSON line on stdout:
   * value / ms_per_step: KDA chunkwise prefill at B=4, T=4096, H=16, dk=dv=128, chunk 64 (bf16 q/k/v, fp32
     per-channel gate, beta and state, initial state ~ N(0, 0.02)); one step = one call of
-    chunk_kimi_delta_attention(..., output_final_state=True) with every input already resident in HBM.
-  * roofline: the fused chunk kernel against HBM (its bound): algorithmic bytes per launch (inputs read once,
-    outputs written once) / average launch time measured with HIP events on the launch stream; traffic = HBM
-    bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary when it matches the current
-    kernel source, else null.  mfma_frac reports the same launch against the dense bf16 MFMA peak.
+    chunk_kimi_delta_attention(..., output_final_state=True) with every input already resident in HBM.  A call
+    is two launches on the caller's stream: the chunk-parallel preparation kernel and the state-scan kernel.
+  * roofline: the call against HBM (its bound): algorithmic bytes per call (inputs read once, outputs written
+    once) / average call time measured with HIP events on the launch stream; traffic = HBM bytes per call (both
+    launches) from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary when it matches the current kernel
+    source, else null.  mfma_frac reports the same call against the dense bf16 MFMA peak.
   * decode: the batch-256 KDA decode step (fp32 state [256,16,128,128] ~ N(0, 0.02), one token per sequence,
     1000 back-to-back steps, state handed from step to step as the reference API does), in state GB/s.
   * cpu_baseline: the reference's CPU path for the op (fp32 token loop, restated in oracle/) timed on this
@@ -93,7 +94,7 @@ def bench_prefill(gdr, workloads, torch, steps, warmup):
             step()
         stop.record(stream)
         torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps  # ms per step (= per launch: one kernel per call)
+    return start.elapsed_time(stop) / steps  # ms per step (one call: prep + scan launches)
 
 
 def bench_decode(gdr, workloads, torch, warmup):

@@ -39,24 +39,28 @@ namespace {
 
 constexpr int kScanSlice = 64;  // value columns per scan workgroup
 
-// Workspace record of one (chunk, head); byte offsets.  UT (U^T, [V][TP]) closes the record.
+// Workspace record of one (chunk, head); byte offsets.  UT (U^T, [V][64]) closes the record.  Rows are unpadded;
+// 16-byte chunks are XOR-swizzled within a row instead (chunk c of row r stored at chunk c ^ (r mod chunks per
+// row)), which keeps every LDS read pattern of the scan kernel free of bank conflicts.
+//   * W and Q e^B are A operands of 16x16x32 MFMAs whose B operand is the state in the two-tile k order: within
+//     each 32-channel group, position 8 g + j holds channel 4 g + j (j < 4) or 16 + 4 g + j - 4 (j >= 4), so a lane
+//     reads its 8 operands with one 16-byte LDS read.
+//   * K e^{B_end - B} is row-major in natural order and read with the transposing LDS read.
 template <int K>
 struct Rec {
-  // W and Q e^B are A operands of 16x16x32 MFMAs whose B operand is the state in the two-tile k order: within
-  // each 32-channel group, stored position 8 g + j holds channel 4 g + j (j < 4) or 16 + 4 g + j - 4 (j >= 4), so
-  // every lane reads its 8 operands with one 16-byte LDS read.  K e^{B_end - B} is read with the transposing LDS
-  // read, which is conflict-free at a row pitch of 8 (mod 64) dwords.
-  static constexpr int KP = K + 8;    // row pitch of W and Q e^B (bf16)
-  static constexpr int KTP = K + 16;  // row pitch of K e^{B_end - B} (bf16)
-  static constexpr int TP = 64 + 8;   // row pitch of [*][64 tokens] bf16 arrays
-  static constexpr int W = 0;                                   // bf16 [64][KP]  A diag(beta) K e^B (permuted)
-  static constexpr int QD = W + 64 * KP * 2;                    // bf16 [64][KP]  scale Q e^B (permuted)
-  static constexpr int KT = QD + 64 * KP * 2;                   // bf16 [64][KTP] K e^{B_end - B}
-  static constexpr int SC = KT + 64 * KTP * 2;                  // bf16 [10][16][16] gated scores, tile (i, j <= i)
+  static constexpr int W = 0;                                   // bf16 [64][K]   A diag(beta) K e^B (permuted)
+  static constexpr int QD = W + 64 * K * 2;                     // bf16 [64][K]   scale Q e^B (permuted)
+  static constexpr int KT = QD + 64 * K * 2;                    // bf16 [64][K]   K e^{B_end - B}
+  static constexpr int SC = KT + 64 * K * 2;                    // bf16 [10][16][16] scale x gated scores, tile (i, j <= i)
   static constexpr int GAM = SC + 10 * 256 * 2;                 // fp32 [K] e^{B_end}
   static constexpr int FIX = ((GAM + K * 4 + 255) / 256) * 256;  // start of UT
-  static constexpr int UT_SLICE = kScanSlice * TP * 2;          // bytes of 64 rows of UT
-  static int64_t bytes(int value_dim) { return FIX + ((int64_t(value_dim) * TP * 2 + 255) / 256) * 256; }
+  static constexpr int UT_SLICE = kScanSlice * 64 * 2;          // bytes of 64 rows of UT
+  static int64_t bytes(int value_dim) { return FIX + ((int64_t(value_dim) * 64 * 2 + 255) / 256) * 256; }
+  // element offsets of (row, column) in the swizzled [*][K] arrays and of (row, token) in UT
+  static __device__ __forceinline__ int rk(int row, int col) {
+    return row * K + (((col >> 3) ^ (row & (K / 8 - 1))) << 3) + (col & 7);
+  }
+  static __device__ __forceinline__ int rt(int row, int tok) { return row * 64 + (((tok >> 3) ^ (row & 7)) << 3) + (tok & 7); }
 };
 
 // LDS of the prep kernel (bytes); 3 workgroups fit a CU for K = 128.
@@ -117,7 +121,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
   constexpr int KS = K / 32;
   using L = PrepLds<K>;
   using R = Rec<K>;
-  constexpr int KP = L::KP, TP = R::TP;
+  constexpr int KP = L::KP;
   constexpr float kHot = kHotSpan * kLog2e;  // hot threshold on -T in log2 units
   extern __shared__ __align__(16) unsigned char smem[];
 
@@ -337,11 +341,11 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
     if constexpr (kDelta) *reinterpret_cast<bf16x8*>(kd + ro) = vkd;
     // scale Q e^B in the permuted channel order: this lane's channels 8 g4 .. 8 g4 + 7 of the group land as two
     // 4-channel pieces at positions pb and pb + 8
-    const int pb = (16 * p + l16) * R::KP + 32 * kk + 16 * (g4 & 1) + 4 * (g4 >> 1);
+    const int pb = 32 * kk + 16 * (g4 & 1) + 4 * (g4 >> 1);
     __bf16* qrec = reinterpret_cast<__bf16*>(rec + R::QD);
-    *reinterpret_cast<bf16x4*>(qrec + pb) = bf16x4{vqd[0], vqd[1], vqd[2], vqd[3]};
-    *reinterpret_cast<bf16x4*>(qrec + pb + 8) = bf16x4{vqd[4], vqd[5], vqd[6], vqd[7]};
-    *reinterpret_cast<bf16x8*>(rec + R::KT + ((16 * p + l16) * R::KTP + ch) * 2) = vkt;  // K e^{B_end - B}
+    *reinterpret_cast<bf16x4*>(qrec + R::rk(16 * p + l16, pb)) = bf16x4{vqd[0], vqd[1], vqd[2], vqd[3]};
+    *reinterpret_cast<bf16x4*>(qrec + R::rk(16 * p + l16, pb + 8)) = bf16x4{vqd[4], vqd[5], vqd[6], vqd[7]};
+    *reinterpret_cast<bf16x8*>(reinterpret_cast<__bf16*>(rec + R::KT) + R::rk(16 * p + l16, ch)) = vkt;
   }
   lds_barrier();
 
@@ -461,12 +465,12 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
           // X_i^T: row 16 i + l16, channels out_col0 + 4 g4 + r, stored in the permuted channel order
           const bf16x4 xt = pack4(mfma16(zb, ai, zero4));
           const int wpos = 32 * (out_col0 >> 5) + 8 * g4 + 4 * ((out_col0 >> 4) & 1);
-          *reinterpret_cast<bf16x4*>(wrec + (16 * i + l16) * R::KP + wpos) = xt;
+          *reinterpret_cast<bf16x4*>(wrec + R::rk(16 * i + l16, wpos)) = xt;
         }
       } else {
         xs[i] = pack4(z);
       }
-      if (!is_w) *reinterpret_cast<bf16x4*>(utrec + (out_col0 + l16) * TP + 16 * i + 4 * g4) = xs[i];
+      if (!is_w) *reinterpret_cast<bf16x4*>(utrec + R::rt(out_col0 + l16, 16 * i + 4 * g4)) = xs[i];
     }
   };
   if constexpr (kDelta) {
@@ -496,7 +500,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
   constexpr bool kDelta = VARIANT != GDR_GLA;
   constexpr int KT = K / 16, KS = K / 32, NT = kScanTiles;
   using R = Rec<K>;
-  constexpr int KP = R::KP, TP = R::TP;
+
   constexpr int SB = R::FIX + R::UT_SLICE;         // LDS bytes per buffer
   constexpr int NF = R::FIX / 16, NU = R::UT_SLICE / 16;
   constexpr int NG = ((NF + NU + 63) / 64 + kScanLoaders - 1) / kScanLoaders;  // 64-piece groups per loader wave
@@ -534,7 +538,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
     const int lw = wave - kScanCompute;
     const unsigned char* rec0 = ws + (int64_t(base) * H + h) * rec_bytes;
     const int64_t rec_stride = int64_t(H) * rec_bytes;
-    const int ut_off = R::FIX + v0 * TP * 2;
+    const int ut_off = R::FIX + v0 * 64 * 2;
     auto copy_record = [&](int chunk, int buf) {
       const unsigned char* src = rec0 + chunk * rec_stride;
       unsigned char* dst = smem + buf * SB;
@@ -583,7 +587,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
     const __bf16* ql = reinterpret_cast<const __bf16*>(bb + R::QD);
     const __bf16* scl = reinterpret_cast<const __bf16*>(bb + R::SC);
     const float* gam = reinterpret_cast<const float*>(bb + R::GAM);
-    const __bf16* utl = reinterpret_cast<const __bf16*>(bb + R::FIX) + (c0 - v0 + l16) * TP;
+    const __bf16* utl = reinterpret_cast<const __bf16*>(bb + R::FIX);  // UT rows of this slice
 
     // state as the bf16 B operand: two accumulator tiles = one 32-deep k slot set {32kk + 4g4 + r, +16}
     bf16x8 sB[NT][KS];
@@ -602,7 +606,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
     auto read_block = [&](int i, int buf) {
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
-        const int r0 = (16 * i + l16) * KP + 32 * kk + 8 * g4;  // permuted order: one 16-byte read
+        const int r0 = R::rk(16 * i + l16, 32 * kk + 8 * g4);  // permuted order: one 16-byte read
         fq[buf][kk] = *reinterpret_cast<const bf16x8*>(ql + r0);
         if constexpr (kDelta) fw[buf][kk] = *reinterpret_cast<const bf16x8*>(wl + r0);
       }
@@ -625,7 +629,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const bf16x4 uu = *reinterpret_cast<const bf16x4*>(utl + 16 * t * TP + 16 * i + 4 * g4);
+        const bf16x4 uu = *reinterpret_cast<const bf16x4*>(utl + R::rt(c0 - v0 + 16 * t + l16, 16 * i + 4 * g4));
         floatx4 u;
 #pragma unroll
         for (int r = 0; r < 4; ++r) u[r] = kDelta ? f32(uu[r]) - ax[t][r] : f32(uu[r]);
@@ -650,8 +654,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
       for (int kk = 0; kk < 2; ++kk) {
         const int tok = 32 * kk + 4 * g4 + (l16 >> 2);
         const int chn = 16 * m + 4 * (l16 & 3);
-        const int off = (s & 1) * SB + R::KT + (tok * R::KTP + chn) * 2;
-        fk[buf][kk] = concat(lds_read_tr(smem, off), lds_read_tr(smem, off + 16 * R::KTP * 2));
+        const int off = (s & 1) * SB + R::KT;
+        fk[buf][kk] = concat(lds_read_tr(smem, off + R::rk(tok, chn) * 2), lds_read_tr(smem, off + R::rk(tok + 16, chn) * 2));
       }
     };
     read_kt(0, 0);
