@@ -92,7 +92,8 @@ int gdr_chunk_fwd(const gdr_args* args, hipStream_t stream);
  * read; no pointer is dereferenced), or a negative gdr_status.  The workspace holds one record per (chunk, head)
  * that the chunk-parallel preparation kernel writes and the state-scan kernel reads: the reference keeps the
  * same kind of intermediates (gate cumsum, P, A, W, U, States) in tensors it allocates per call
- * (src/ops/kimi_delta_attention.py:540-553).  For B=4, T=4096, H=16, K=V=128 it is 317 MB. */
+ * (src/ops/kimi_delta_attention.py:540-553).  For B=4, T=4096, H=16, K=V=128 it is 291.5 MB (71,168 bytes per
+ * chunk and head). */
 int64_t gdr_chunk_workspace_bytes(const gdr_args* args);
 
 /* Recurrent forward (decode).  Replaces the `_recurrent_forward` Triton launch of
