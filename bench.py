@@ -33,6 +33,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PREFILL = dict(B=4, T=4096, H=16, K=128, V=128, chunk=64)
 DECODE = dict(B=256, H=16, K=128, V=128, steps=1000)
+VARLEN = dict(n_seqs=32, low=256, high=4096, H=16, K=128, V=128)
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 
 
@@ -128,6 +129,36 @@ def bench_decode(gdr, workloads, torch, warmup):
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": committed_traffic("recurrent_kda_decode")}}
 
 
+def bench_varlen(gdr, workloads, torch, steps, warmup):
+    """The packed-prefill configuration's KDA op: 32 sequences with lengths ~U[256, 4096] (seeded) packed via
+    cu_seqlens, H=16, dk=dv=128, per-sequence initial state ~ N(0, 0.02)."""
+    cfg = VARLEN
+    lengths = workloads.varlen_lengths(cfg["n_seqs"], cfg["low"], cfg["high"], seed=0)
+    inp, cu = workloads.make_varlen_inputs("kda", lengths, cfg["H"], cfg["K"], cfg["V"], seed=0, device="cuda")
+    args = inp.args()
+
+    def step():
+        return gdr.chunk_kimi_delta_attention(*args, initial_state=inp.initial_state, output_final_state=True,
+                                              cu_seqlens=cu)
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            step()
+        stop.record(stream)
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    tokens = sum(lengths)
+    return {"workload": "kda_varlen_packed_prefill", "n_seqs": cfg["n_seqs"], "tokens": tokens, "H": cfg["H"],
+            "K": cfg["K"], "V": cfg["V"], "ms_per_call": round(ms, 4), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+            "note": "KDA op only (the layer stack around it is out of scope)"}
+
+
 def cpu_baseline(workloads, torch, budget_s):
     """The reference CPU path (fp32 token loop) on the full prefill workload, repeated until `budget_s`."""
     from oracle import gdr_oracle as oracle
@@ -156,6 +187,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-varlen", action="store_true", help="skip the packed varlen prefill leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="minimum seconds of CPU baseline work")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the GPU legs, copy a buffer of this many MiB three times (a plain copy kernel of "
@@ -204,6 +236,8 @@ def main():
     }
     if not opts.no_decode:
         record["decode"] = bench_decode(gdr, workloads, torch, warmup=20)
+    if not opts.no_varlen:
+        record["varlen"] = bench_varlen(gdr, workloads, torch, steps=10, warmup=3)
     if opts.copy_mib:
         src = torch.ones(opts.copy_mib * 2**18, device="cuda")
         dst = torch.empty_like(src)

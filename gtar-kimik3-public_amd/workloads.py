@@ -85,3 +85,23 @@ def decode_state(batch: int, heads: int, key_dim: int, value_dim: int, *, std: f
     for b in range(batch):
         out[b].copy_(torch.randn(heads, key_dim, value_dim, generator=gen, dtype=torch.float32) * std)
     return out
+
+
+def varlen_lengths(n_seqs: int = 32, low: int = 256, high: int = 4096, *, seed: int = 0) -> list[int]:
+    """Sequence lengths ~ U[low, high] (inclusive), seeded: the packed-prefill configuration's length mix."""
+    gen = torch.Generator("cpu").manual_seed(seed)
+    return [int(x) for x in torch.randint(low, high + 1, (n_seqs,), generator=gen)]
+
+
+def make_varlen_inputs(variant: str, lengths: list[int], heads: int, key_dim: int, value_dim: int, *, seed: int = 0,
+                       dtype=torch.bfloat16, state_std: float | None = 0.02, device="cpu"):
+    """Packed [1, H, sum(lengths), D] inputs with int32 `cu_seqlens` [N + 1] and a per-sequence initial state
+    [N, H, K, V] (None when `state_std` is None).  Returns (Inputs, cu_seqlens)."""
+    total = sum(lengths)
+    inp = make_inputs(variant, 1, total, heads, key_dim, value_dim, seed=seed, dtype=dtype, device=device)
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32, device=device)
+    if state_std is not None:
+        gen = torch.Generator("cpu").manual_seed(seed + 1)
+        inp.initial_state = (torch.randn(len(lengths), heads, key_dim, value_dim, generator=gen,
+                                         dtype=torch.float32) * state_std).to(device)
+    return inp, cu

@@ -162,3 +162,19 @@ def test_chunk_without_workspace_matches_oracle(variant):
     q, k, v, g, beta, h0 = oracle_args(inp)
     ref_o, ref_s = oracle.chunkwise(variant, q, k, v, g, beta, None, h0)
     assert out_error(out, ref_o) <= OUT_TOL and state_error(ht, ref_s) <= STATE_TOL
+
+
+def test_chunk_varlen_packed_prefill_config():
+    """Packed-prefill configuration's length mix (32 sequences, lengths ~U[256, 4096]) at H=2, KDA."""
+    lengths = workloads.varlen_lengths(32, 256, 4096, seed=0)
+    print(f"varlen KDA 32 seqs, {sum(lengths)} tokens, H=2", flush=True)
+    inp, cu = workloads.make_varlen_inputs("kda", lengths, 2, 128, 128, seed=0, device="cuda")
+    with torch.no_grad():
+        out, state = CHUNK_FNS["kda"](*inp.args(), initial_state=inp.initial_state, output_final_state=True,
+                                      cu_seqlens=cu)
+    torch.cuda.synchronize()
+    q, k, v, g, beta, h0 = oracle_args(inp)
+    ref_o, ref_s = oracle.varlen(oracle.chunkwise, "kda", q, k, v, g, beta, None, h0, cu.cpu())
+    eo, es = out_error(out, ref_o), state_error(state, ref_s)
+    print(f"varlen packed config: out err {eo:.2e} state err {es:.2e}", flush=True)
+    assert eo <= OUT_TOL and es <= STATE_TOL
