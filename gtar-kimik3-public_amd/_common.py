@@ -7,9 +7,14 @@ gated_deltanet.py:472-520, gated_linear_attention.py:437-483, deltanet.py:399-44
   * a missing initial state is a zero fp32 state, a given one is used as `initial_state.float().contiguous()`,
   * the final state is always a fresh fp32 tensor and inputs are never modified,
   * the output has the value's dtype; `(out, final_state)` is returned only when `output_final_state`.
+The chunk ops are differentiable like the reference's torch.autograd.Function classes
+(kimi_delta_attention.py:534-622 and its twins): when an input requires grad, the forward runs through
+`_ChunkFunction`, whose backward is libgdr's gdr_chunk_bwd, returning gradients for q, k, v, gate, beta and the
+initial state (none for `scale`).
 Differences, all deliberate: CPU tensors raise (the reference's CPU token loop is this repository's test oracle,
-not a product path); requesting gradients raises (the forward-only kernels have no backward yet); packed
-variable-length input is accepted through `cu_seqlens` (the reference has none).
+not a product path); gradients through the recurrent ops raise (the reference's recurrent ops have none either)
+and so do gradients of packed varlen calls; packed variable-length input is accepted through `cu_seqlens` (the
+reference has none).
 """
 
 from __future__ import annotations
@@ -29,11 +34,8 @@ def _autocast(*tensors):
     return list(tensors)
 
 
-def _check_no_grad(*tensors):
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
-        raise NotImplementedError(
-            "the gfx950 gated delta-rule kernels are forward-only; run under torch.no_grad() or detach the inputs"
-        )
+def _wants_grad(*tensors) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors)
 
 
 def _aligned(x: torch.Tensor) -> bool:
@@ -50,7 +52,12 @@ def _as_row_aligned(x: torch.Tensor) -> torch.Tensor:
 def run(variant: int, chunk: bool, query, key, value, gate, beta, scale, initial_state, output_final_state,
         cu_seqlens=None):
     name = _VARIANT_NAMES[variant]
-    _check_no_grad(query, key, value, gate, beta, initial_state)
+    grad = _wants_grad(query, key, value, gate, beta, initial_state)
+    if grad and not chunk:
+        raise NotImplementedError(f"{name}: the recurrent op has no backward (as in the reference); use the chunk op "
+                                  "for training or run under torch.no_grad()")
+    if grad and cu_seqlens is not None:
+        raise NotImplementedError(f"{name}: the chunk backward does not take packed varlen input (cu_seqlens)")
     tensors = [t for t in (query, key, value, gate, beta, initial_state, cu_seqlens) if t is not None]
     if not all(t.is_cuda for t in tensors):
         raise ValueError(f"{name}: all tensors must be on the GPU (this implementation has no CPU path)")
@@ -105,9 +112,52 @@ def run(variant: int, chunk: bool, query, key, value, gate, beta, scale, initial
         if gate is not None and variant != _lib.GDN:
             gate = _as_row_aligned(gate)
 
+    if grad:
+        out, final_state = _ChunkFunction.apply(variant, query, key, value, gate, beta, scale, initial_state,
+                                                out_dtype)
+        return (out, final_state) if output_final_state else out
+
     out = torch.empty(batch, heads, seq_len, value_dim, device=device, dtype=out_dtype)
     final_state = torch.empty(state_shape, device=device, dtype=torch.float32) if output_final_state else None
     args = _lib.make_args(variant, query, key, value, gate, beta, out, scale, initial_state, final_state, cu_seqlens)
     workspace = _lib.chunk_workspace(args, device) if chunk else None  # noqa: F841 (alive until enqueued)
     _lib.launch("gdr_chunk_fwd" if chunk else "gdr_recurrent_fwd", args, device)
     return (out, final_state) if output_final_state else out
+
+
+class _ChunkFunction(torch.autograd.Function):
+    """Chunk forward + gdr_chunk_bwd.  Inputs arrive resolved by `run`: bf16 q, k, v with 16-byte rows, fp32
+    gate / beta, fp32 contiguous initial state (or None).  Saves the inputs only; the backward recomputes the
+    per-chunk states, as the reference's backward does (kimi_delta_attention.py:555, :566-571)."""
+
+    @staticmethod
+    def forward(ctx, variant, query, key, value, gate, beta, scale, initial_state, out_dtype):
+        batch, heads, seq_len, key_dim = query.shape
+        value_dim = value.shape[-1]
+        device = query.device
+        out = torch.empty(batch, heads, seq_len, value_dim, device=device, dtype=out_dtype)
+        final_state = torch.empty(batch, heads, key_dim, value_dim, device=device, dtype=torch.float32)
+        args = _lib.make_args(variant, query, key, value, gate, beta, out, scale, initial_state, final_state)
+        workspace = _lib.chunk_workspace(args, device)  # noqa: F841 (alive until enqueued)
+        _lib.launch("gdr_chunk_fwd", args, device)
+        ctx.save_for_backward(query, key, value, gate, beta, initial_state)
+        ctx.variant, ctx.scale = variant, scale
+        return out, final_state
+
+    @staticmethod
+    def backward(ctx, d_out, d_final):
+        query, key, value, gate, beta, initial_state = ctx.saved_tensors
+        device = query.device
+        if d_out is None:
+            d_out = torch.zeros(value.shape, device=device, dtype=torch.bfloat16)
+        d_out = _as_row_aligned(d_out.to(torch.bfloat16))
+        if d_final is not None:
+            d_final = d_final.float().contiguous()
+        dq, dk, dv = torch.empty_like(query), torch.empty_like(key), torch.empty_like(value)
+        dg = torch.empty_like(gate) if gate is not None else None
+        db = torch.empty_like(beta) if beta is not None else None
+        dh0 = torch.empty_like(initial_state) if initial_state is not None else None
+        args = _lib.make_args(ctx.variant, query, key, value, gate, beta, None, ctx.scale, initial_state, None)
+        grads = _lib.make_grads(d_out, d_final, dq, dk, dv, dg, db, dh0)
+        _lib.chunk_backward(args, grads, device)
+        return None, dq, dk, dv, dg, db, None, dh0, None

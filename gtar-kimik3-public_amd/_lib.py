@@ -18,7 +18,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.join(_HERE, "libgdr.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 KDA, GDN, GLA, DELTANET = 0, 1, 2, 3
 F32, BF16, F16 = 0, 1, 2
@@ -62,8 +62,24 @@ class GdrArgs(ctypes.Structure):
     ]
 
 
+class GdrGrads(ctypes.Structure):
+    _fields_ = [
+        ("d_out", GdrTensor),
+        ("d_final", ctypes.c_void_p),
+        ("d_query", GdrTensor),
+        ("d_key", GdrTensor),
+        ("d_value", GdrTensor),
+        ("d_gate", GdrTensor),
+        ("d_beta", GdrTensor),
+        ("d_initial", ctypes.c_void_p),
+    ]
+
+
 # Every symbol include/gdr.h declares, with its ctypes signature.
 EXPORTS = {
+    "gdr_chunk_bwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.POINTER(GdrGrads), ctypes.c_void_p,
+                                     ctypes.c_int64, ctypes.c_void_p]),
+    "gdr_chunk_bwd_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(GdrArgs)]),
     "gdr_chunk_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
     "gdr_chunk_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(GdrArgs)]),
     "gdr_recurrent_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
@@ -153,3 +169,29 @@ def launch(entry: str, args: GdrArgs, device: torch.device) -> None:
     rc = getattr(lib, entry)(ctypes.byref(args), ctypes.c_void_p(stream))
     if rc != 0:
         raise RuntimeError(f"{entry} failed ({rc}): {lib.gdr_last_error().decode()}")
+
+
+def make_grads(d_out, d_final, d_query, d_key, d_value, d_gate, d_beta, d_initial) -> GdrGrads:
+    grads = GdrGrads()
+    grads.d_out = _view(d_out, "d_out")
+    grads.d_final = d_final.data_ptr() if d_final is not None else None
+    grads.d_query, grads.d_key, grads.d_value = (_view(d_query, "d_query"), _view(d_key, "d_key"),
+                                                 _view(d_value, "d_value"))
+    grads.d_gate, grads.d_beta = _view(d_gate, "d_gate"), _view(d_beta, "d_beta")
+    grads.d_initial = d_initial.data_ptr() if d_initial is not None else None
+    return grads
+
+
+def chunk_backward(args: GdrArgs, grads: GdrGrads, device: torch.device) -> None:
+    """Allocate the backward workspace from torch's caching allocator and enqueue gdr_chunk_bwd on torch's current
+    stream (the workspace tensor is released to the allocator, which orders reuse on that stream)."""
+    lib = load_library()
+    nbytes = lib.gdr_chunk_bwd_workspace_bytes(ctypes.byref(args))
+    if nbytes < 0:
+        raise RuntimeError(f"gdr_chunk_bwd_workspace_bytes failed ({nbytes}): {lib.gdr_last_error().decode()}")
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    rc = lib.gdr_chunk_bwd(ctypes.byref(args), ctypes.byref(grads), ctypes.c_void_p(ws.data_ptr()),
+                           ctypes.c_int64(int(nbytes)), ctypes.c_void_p(stream))
+    if rc != 0:
+        raise RuntimeError(f"gdr_chunk_bwd failed ({rc}): {lib.gdr_last_error().decode()}")

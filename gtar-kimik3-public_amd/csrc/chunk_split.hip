@@ -30,38 +30,13 @@
 // reference stores W, U and u.
 #include "chunk_common.h"
 #include "gdr_internal.h"
+#include "split_common.h"
 
 namespace gdr {
 
 using namespace chunk;
 
 namespace {
-
-constexpr int kScanSlice = 64;  // value columns per scan workgroup
-
-// Workspace record of one (chunk, head); byte offsets.  UT (U^T, [V][64]) closes the record.  Rows are unpadded;
-// 16-byte chunks are XOR-swizzled within a row instead (chunk c of row r stored at chunk c ^ (r mod chunks per
-// row)), which keeps every LDS read pattern of the scan kernel free of bank conflicts.
-//   * W and Q e^B are A operands of 16x16x32 MFMAs whose B operand is the state in the two-tile k order: within
-//     each 32-channel group, position 8 g + j holds channel 4 g + j (j < 4) or 16 + 4 g + j - 4 (j >= 4), so a lane
-//     reads its 8 operands with one 16-byte LDS read.
-//   * K e^{B_end - B} is row-major in natural order and read with the transposing LDS read.
-template <int K>
-struct Rec {
-  static constexpr int W = 0;                                   // bf16 [64][K]   A diag(beta) K e^B (permuted)
-  static constexpr int QD = W + 64 * K * 2;                     // bf16 [64][K]   scale Q e^B (permuted)
-  static constexpr int KT = QD + 64 * K * 2;                    // bf16 [64][K]   K e^{B_end - B}
-  static constexpr int SC = KT + 64 * K * 2;                    // bf16 [10][16][16] scale x gated scores, tile (i, j <= i)
-  static constexpr int GAM = SC + 10 * 256 * 2;                 // fp32 [K] e^{B_end}
-  static constexpr int FIX = ((GAM + K * 4 + 255) / 256) * 256;  // start of UT
-  static constexpr int UT_SLICE = kScanSlice * 64 * 2;          // bytes of 64 rows of UT
-  static int64_t bytes(int value_dim) { return FIX + ((int64_t(value_dim) * 64 * 2 + 255) / 256) * 256; }
-  // element offsets of (row, column) in the swizzled [*][K] arrays and of (row, token) in UT
-  static __device__ __forceinline__ int rk(int row, int col) {
-    return row * K + (((col >> 3) ^ (row & (K / 8 - 1))) << 3) + (col & 7);
-  }
-  static __device__ __forceinline__ int rt(int row, int tok) { return row * 64 + (((tok >> 3) ^ (row & 7)) << 3) + (tok & 7); }
-};
 
 // LDS of the prep kernel (bytes); 3 workgroups fit a CU for K = 128.
 template <int K>
@@ -84,34 +59,6 @@ struct PrepLds {
   static_assert(8 * K * 4 <= 16 * 512, "EPRE/ETAIL alias");
   static_assert(4 * 512 <= 11 * K * 4, "AINV alias");
 };
-
-// Inclusive prefix sum over the 16 lanes of each DPP row (v_add_f32 with row_shr:1, 2, 4, 8; lanes shifted in from
-// outside the row contribute 0).
-__device__ __forceinline__ float row_scan16(float x) {
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, true));
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, true));
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, true));
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, true));
-  return x;
-}
-
-// Four consecutive outputs in one 8-byte (16-bit types) or 16-byte (fp32) store.
-__device__ __forceinline__ void store4(__bf16* dst, floatx4 v) {
-  *reinterpret_cast<bf16x4*>(dst) = bf16x4{bf(v[0]), bf(v[1]), bf(v[2]), bf(v[3])};
-}
-__device__ __forceinline__ void store4(_Float16* dst, floatx4 v) {
-  typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4;
-  *reinterpret_cast<f16x4*>(dst) = f16x4{static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]),
-                                         static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
-}
-__device__ __forceinline__ void store4(float* dst, floatx4 v) {
-  *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-}
-
-// First workspace slot of packed sequence n: floor(bos / 64) + n.  Slots of consecutive sequences never
-// overlap (floor(a + b) >= floor(a) + floor(b) and floor(len / 64) + 1 >= ceil(len / 64)) and every slot is below
-// ceil(T / 64) + n_seqs.
-__device__ __forceinline__ int varlen_base(const int32_t* cu, int n) { return cu[n] / kChunk + n; }
 
 // ======================================= prep: one workgroup per (chunk, head) =======================================
 template <int VARIANT, int K>
@@ -494,9 +441,13 @@ constexpr int kScanCompute = kScanSlice / (16 * kScanTiles);  // compute waves p
 constexpr int kScanLoaders = 4;                        // loader waves per scan workgroup
 constexpr int kScanThreads = 64 * (kScanCompute + kScanLoaders);
 
-template <int VARIANT, int K, typename OutT>
+// kStates (backward recompute): instead of the output, write the fp32 state entering every chunk (and the final
+// one) to `states` [NC + 1][K][V] and the bf16 u to `ubuf` [NC * 64][V], per (sequence, head).
+template <int VARIANT, int K, typename OutT, bool kStates = false>
 __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_args a, int n_slices, int xcd_map,
-                                                                     int nc, int64_t rec_bytes) {
+                                                                     int nc, int64_t rec_bytes,
+                                                                     float* __restrict__ states,
+                                                                     __bf16* __restrict__ ubuf) {
   constexpr bool kDelta = VARIANT != GDR_GLA;
   constexpr int KT = K / 16, KS = K / 32, NT = kScanTiles;
   using R = Rec<K>;
@@ -581,8 +532,22 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
         st[t][m][r] = a.h0 ? a.h0[sbase + size_t(16 * m + 4 * g4 + r) * a.value_dim + c0 + 16 * t + l16] : 0.f;
   lds_barrier();
 
+  const int V = a.value_dim;
+  const size_t st_base = size_t(n * H + h) * (nc + 1) * K * V;  // kStates buffers (non-varlen only)
+  const size_t ub_base = size_t(n * H + h) * nc * kChunk * V;
+  auto store_state = [&](int c) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int m = 0; m < KT; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          states[st_base + (size_t(c) * K + 16 * m + 4 * g4 + r) * V + c0 + 16 * t + l16] = st[t][m][r];
+  };
+
   for (int s = 0; s < nchunks; ++s) {
     const unsigned char* bb = smem + (s & 1) * SB;
+    if constexpr (kStates) store_state(s);
     const __bf16* wl = reinterpret_cast<const __bf16*>(bb + R::W);
     const __bf16* ql = reinterpret_cast<const __bf16*>(bb + R::QD);
     const __bf16* scl = reinterpret_cast<const __bf16*>(bb + R::SC);
@@ -607,7 +572,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
         const int r0 = R::rk(16 * i + l16, 32 * kk + 8 * g4);  // permuted order: one 16-byte read
-        fq[buf][kk] = *reinterpret_cast<const bf16x8*>(ql + r0);
+        if constexpr (!kStates) fq[buf][kk] = *reinterpret_cast<const bf16x8*>(ql + r0);
         if constexpr (kDelta) fw[buf][kk] = *reinterpret_cast<const bf16x8*>(wl + r0);
       }
     };
@@ -623,7 +588,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
       for (int kk = 0; kk < KS; ++kk) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          ao[t] = mfma32(sB[t][kk], fq[i & 1][kk], ao[t]);
+          if constexpr (!kStates) ao[t] = mfma32(sB[t][kk], fq[i & 1][kk], ao[t]);
           if constexpr (kDelta) ax[t] = mfma32(fw[i & 1][kk], sB[t][kk], ax[t]);
         }
       }
@@ -635,18 +600,25 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
         for (int r = 0; r < 4; ++r) u[r] = kDelta ? f32(uu[r]) - ax[t][r] : f32(uu[r]);
         ub[t][i] = pack4(u);
         acc_ot[t][i] = ao[t];
+        if constexpr (kStates) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            ubuf[ub_base + size_t(s * kChunk + 16 * i + 4 * g4 + r) * V + c0 + 16 * t + l16] = ub[t][i][r];
+        }
       }
     }
     // O_i^T += u_j^T Sc_ij^T: u_j's accumulator layout is the A layout of u_j^T; Sc_ij^T is read like Sc_ij as A
-    bf16x4 fsc[10];
+    if constexpr (!kStates) {
+      bf16x4 fsc[10];
 #pragma unroll
-    for (int q = 0; q < 10; ++q) fsc[q] = *reinterpret_cast<const bf16x4*>(scl + q * 256 + l16 * 16 + 4 * g4);
+      for (int q = 0; q < 10; ++q) fsc[q] = *reinterpret_cast<const bf16x4*>(scl + q * 256 + l16 * 16 + 4 * g4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j <= i; ++j)
+        for (int j = 0; j <= i; ++j)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc_ot[t][i] = mfma16(ub[t][j], fsc[tri_tile(i, j)], acc_ot[t][i]);
+          for (int t = 0; t < NT; ++t) acc_ot[t][i] = mfma16(ub[t][j], fsc[tri_tile(i, j)], acc_ot[t][i]);
+    }
     // S = diag(gamma) S + Kt^T u, Kt^T read transposed from the row-major tile, one tile ahead
     bf16x8 fk[2][2];
     auto read_kt = [&](int m, int buf) {
@@ -677,13 +649,14 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tk = s * kChunk + 16 * i + l16;
-      if (tk < len) {
+      if (!kStates && tk < len) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) store4(op + tk * o_st + c0 + 16 * t + 4 * g4, acc_ot[t][i]);
       }
     }
     lds_barrier();
   }
+  if constexpr (kStates) store_state(nchunks);
   if (a.ht) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -725,7 +698,7 @@ hipError_t launch_split_typed(const gdr_args& a, hipStream_t stream) {
   const int n_slices = a.value_dim / kScanSlice;
   const int xcd_map = (bh % 8 == 0) ? 1 : 0;
   hipLaunchKernelGGL((chunk_scan_kernel<VARIANT, K, OutT>), dim3(bh * n_slices), dim3(kScanThreads), scan_lds,
-                     stream, a, n_slices, xcd_map, nc, rec);
+                     stream, a, n_slices, xcd_map, nc, rec, nullptr, nullptr);
   return hipGetLastError();
 }
 
@@ -743,11 +716,59 @@ hipError_t launch_split_v(const gdr_args& a, hipStream_t stream) {
   return a.key_dim == 64 ? launch_split_k<VARIANT, 64>(a, stream) : launch_split_k<VARIANT, 128>(a, stream);
 }
 
+// Backward recompute: records into the backward workspace, then the scan in its states mode.
+template <int VARIANT, int K>
+hipError_t launch_states_typed(const gdr_args& fwd, const BwdLayout& L, unsigned char* ws, hipStream_t stream) {
+  gdr_args a = fwd;
+  a.workspace = ws + L.rec;
+  a.ht = nullptr;
+  const int nc = (a.seq_len + kChunk - 1) / kChunk;
+  const int64_t rec = Rec<K>::bytes(a.value_dim);
+  const int64_t n_prep = slots_per_head(a) * a.heads;
+  constexpr int prep_lds = PrepLds<K>::BYTES;
+  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::UT_SLICE);
+  static bool configured = false;  // benign race: every thread sets the same attributes
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_prep_kernel<VARIANT, K>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, prep_lds);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_scan_kernel<VARIANT, K, __bf16, true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, scan_lds);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  if (n_prep > 0)
+    hipLaunchKernelGGL((chunk_prep_kernel<VARIANT, K>), dim3(unsigned(n_prep)), dim3(256), prep_lds, stream, a, nc,
+                       rec);
+  const int bh = a.batch * a.heads;
+  const int n_slices = a.value_dim / kScanSlice;
+  const int xcd_map = (bh % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL((chunk_scan_kernel<VARIANT, K, __bf16, true>), dim3(bh * n_slices), dim3(kScanThreads),
+                     scan_lds, stream, a, n_slices, xcd_map, nc, rec, reinterpret_cast<float*>(ws + L.states),
+                     reinterpret_cast<__bf16*>(ws + L.ubuf));
+  return hipGetLastError();
+}
+
+template <int VARIANT>
+hipError_t launch_states_v(const gdr_args& a, const BwdLayout& L, unsigned char* ws, hipStream_t stream) {
+  return a.key_dim == 64 ? launch_states_typed<VARIANT, 64>(a, L, ws, stream)
+                         : launch_states_typed<VARIANT, 128>(a, L, ws, stream);
+}
+
 }  // namespace
 
 int64_t chunk_workspace_bytes(const gdr_args& a) {
   const int64_t rec = a.key_dim == 64 ? Rec<64>::bytes(a.value_dim) : Rec<128>::bytes(a.value_dim);
   return slots_per_head(a) * a.heads * rec;
+}
+
+hipError_t launch_chunk_states(const gdr_args& a, const BwdLayout& L, unsigned char* ws, hipStream_t stream) {
+  switch (a.variant) {
+    case GDR_KDA: return launch_states_v<GDR_KDA>(a, L, ws, stream);
+    case GDR_GDN: return launch_states_v<GDR_GDN>(a, L, ws, stream);
+    case GDR_GLA: return launch_states_v<GDR_GLA>(a, L, ws, stream);
+    default: return launch_states_v<GDR_DELTANET>(a, L, ws, stream);
+  }
 }
 
 hipError_t launch_chunk_split(const gdr_args& a, hipStream_t stream) {

@@ -57,7 +57,7 @@ int check_shape(const gdr_args* a, bool chunk) {
   return GDR_OK;
 }
 
-int check_common(const gdr_args* a, bool chunk) {
+int check_common(const gdr_args* a, bool chunk, bool need_out = true) {
   int rc = check_shape(a, chunk);
   if (rc) return rc;
   const bool has_gate = a->variant != GDR_DELTANET;
@@ -65,13 +65,21 @@ int check_common(const gdr_args* a, bool chunk) {
   if ((rc = check_view(a->q, "query", true, false))) return rc;
   if ((rc = check_view(a->k, "key", true, false))) return rc;
   if ((rc = check_view(a->v, "value", true, false))) return rc;
-  if ((rc = check_view(a->out, "out", true, false))) return rc;
+  if ((rc = check_view(a->out, "out", need_out, false))) return rc;
   if ((rc = check_view(a->gate, "gate", has_gate, true))) return rc;
   if ((rc = check_view(a->beta, "beta", has_beta, true))) return rc;
   if (!has_gate && a->gate.ptr) return fail(GDR_ERR_INVALID, "DeltaNet takes no gate");
   if (!has_beta && a->beta.ptr) return fail(GDR_ERR_INVALID, "GLA takes no beta");
   if ((reinterpret_cast<uintptr_t>(a->h0) | reinterpret_cast<uintptr_t>(a->ht)) % 16 != 0)
     return fail(GDR_ERR_INVALID, "initial/final state must be 16-byte aligned");
+  return GDR_OK;
+}
+
+int check_rows16(const gdr_tensor& t, const char* name) {
+  const int es = elem_size(t.dtype);
+  if (reinterpret_cast<uintptr_t>(t.ptr) % 16 || (t.stride_b * es) % 16 || (t.stride_h * es) % 16 ||
+      (t.stride_t * es) % 16)
+    return fail(GDR_ERR_INVALID, "%s: base pointer and b/h/t strides must be 16-byte aligned", name);
   return GDR_OK;
 }
 
@@ -133,6 +141,59 @@ int gdr_chunk_fwd(const gdr_args* a, hipStream_t stream) {
     e = gdr::launch_chunk(*a, stream);
   }
   if (e != hipSuccess) return fail(GDR_ERR_HIP, "chunk launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
+int64_t gdr_chunk_bwd_workspace_bytes(const gdr_args* a) {
+  const int rc = check_shape(a, true);
+  if (rc) return rc;
+  if (a->cu_seqlens) return fail(GDR_ERR_UNSUPPORTED, "the chunk backward does not take packed varlen input");
+  g_last_error.clear();
+  return gdr::chunk_bwd_layout(*a).total;
+}
+
+int gdr_chunk_bwd(const gdr_args* a, const gdr_grads* g, void* workspace, int64_t workspace_bytes,
+                  hipStream_t stream) {
+  int rc = check_common(a, true, false);
+  if (rc) return rc;
+  if (!g) return fail(GDR_ERR_INVALID, "grads is NULL");
+  if (a->cu_seqlens) return fail(GDR_ERR_UNSUPPORTED, "the chunk backward does not take packed varlen input");
+  if (a->q.dtype != GDR_BF16 || a->k.dtype != GDR_BF16 || a->v.dtype != GDR_BF16)
+    return fail(GDR_ERR_UNSUPPORTED, "chunk mode reads bf16 q, k, v (got dtype codes %d, %d, %d)", a->q.dtype,
+                a->k.dtype, a->v.dtype);
+  const bool has_gate = a->variant != GDR_DELTANET, has_beta = a->variant != GDR_GLA;
+  if ((rc = check_view(g->d_out, "d_out", true, false))) return rc;
+  if (g->d_out.dtype != GDR_BF16) return fail(GDR_ERR_UNSUPPORTED, "d_out must be bf16 (the MFMA operand type)");
+  if ((rc = check_view(g->d_query, "d_query", true, false))) return rc;
+  if ((rc = check_view(g->d_key, "d_key", true, false))) return rc;
+  if ((rc = check_view(g->d_value, "d_value", true, false))) return rc;
+  const gdr_tensor* outs[] = {&g->d_query, &g->d_key, &g->d_value};
+  const char* onames[] = {"d_query", "d_key", "d_value"};
+  for (int i = 0; i < 3; ++i)
+    if (outs[i]->dtype == GDR_F16) return fail(GDR_ERR_UNSUPPORTED, "%s: bf16 or f32 only", onames[i]);
+  if ((rc = check_view(g->d_gate, "d_gate", has_gate, true))) return rc;
+  if ((rc = check_view(g->d_beta, "d_beta", has_beta, true))) return rc;
+  if (!has_gate && g->d_gate.ptr) return fail(GDR_ERR_INVALID, "DeltaNet has no gate gradient");
+  if (!has_beta && g->d_beta.ptr) return fail(GDR_ERR_INVALID, "GLA has no beta gradient");
+  if ((reinterpret_cast<uintptr_t>(g->d_final) | reinterpret_cast<uintptr_t>(g->d_initial)) % 16 != 0)
+    return fail(GDR_ERR_INVALID, "d_final / d_initial must be 16-byte aligned");
+  const gdr_tensor* rows[] = {&a->q, &a->k, &a->v, &a->gate, &g->d_out};
+  const char* names[] = {"query", "key", "value", "gate", "d_out"};
+  for (int i = 0; i < 5; ++i) {
+    if (!rows[i]->ptr || (i == 3 && a->variant == GDR_GDN)) continue;
+    if ((rc = check_rows16(*rows[i], names[i]))) return rc;
+  }
+  const gdr::BwdLayout L = gdr::chunk_bwd_layout(*a);
+  if (!workspace) return fail(GDR_ERR_INVALID, "the chunk backward needs a workspace");
+  if (workspace_bytes < L.total)
+    return fail(GDR_ERR_INVALID, "workspace of %lld bytes given, %lld required", (long long)workspace_bytes,
+                (long long)L.total);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(GDR_ERR_INVALID, "workspace must be 256-byte aligned");
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  hipError_t e = gdr::launch_chunk_states(*a, L, ws, stream);
+  if (e == hipSuccess) e = gdr::launch_chunk_bwd(*a, *g, L, ws, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "chunk backward launch failed: %s", hipGetErrorString(e));
   g_last_error.clear();
   return GDR_OK;
 }

@@ -18,4 +18,26 @@ hipError_t launch_chunk(const gdr_args& a, hipStream_t stream);
 int64_t chunk_workspace_bytes(const gdr_args& a);
 hipError_t launch_chunk_split(const gdr_args& a, hipStream_t stream);
 
+// Byte offsets of the chunkwise-backward buffers inside its workspace (each 256-aligned).  Per (sequence, head):
+//   rec      the forward records (chunk_workspace_bytes layout)
+//   states   fp32 [NC + 1][K][V]  state entering each chunk (the last one is the final state)
+//   dstates  fp32 [NC + 1][K][V]  gradient of each of those states
+//   ubuf     bf16 [NC * 64][V]    u = U - W S per chunk row
+//   dubuf    bf16 [NC * 64][V]    its gradient
+//   dqd, dw, dkt  fp32 [NC * 64][K]  dO S^T, -du S^T, u dS'^T per chunk
+//   dsc      fp32 [NC][64][64]   tril(dO u^T) per chunk
+//   bnd      fp32 [NC][K]        rowsum(S (x) dS') per chunk (S entering it, dS' leaving it)
+struct BwdLayout {
+  int64_t rec, states, dstates, ubuf, dubuf, dqd, dw, dkt, dsc, bnd, total;
+};
+BwdLayout chunk_bwd_layout(const gdr_args& a);
+
+// Forward recompute for the backward: the preparation launch, then the state scan in its states mode (writes
+// states and ubuf instead of the output).  `ws` is the backward workspace.
+hipError_t launch_chunk_states(const gdr_args& a, const BwdLayout& L, unsigned char* ws, hipStream_t stream);
+
+// The backward proper (after launch_chunk_states): reverse state scan, state-side products, chunk-local gradients.
+hipError_t launch_chunk_bwd(const gdr_args& a, const gdr_grads& g, const BwdLayout& L, unsigned char* ws,
+                            hipStream_t stream);
+
 }  // namespace gdr

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GDR_ABI_VERSION 2
+#define GDR_ABI_VERSION 3
 
 typedef enum gdr_variant { GDR_KDA = 0, GDR_GDN = 1, GDR_GLA = 2, GDR_DELTANET = 3 } gdr_variant;
 
@@ -95,6 +95,37 @@ int gdr_chunk_fwd(const gdr_args* args, hipStream_t stream);
  * (src/ops/kimi_delta_attention.py:540-553).  For B=4, T=4096, H=16, K=V=128 it is 291.5 MB (71,168 bytes per
  * chunk and head). */
 int64_t gdr_chunk_workspace_bytes(const gdr_args* args);
+
+/* Gradients of gdr_chunk_fwd for gdr_chunk_bwd.  Every tensor has the shape of its forward counterpart;
+ * d_query, d_key and d_value are bf16 or f32 (any of them may differ from the forward dtype), d_gate and
+ * d_beta are f32.  d_final (the gradient of the final state) may be NULL for zero; d_initial may be NULL when
+ * the initial state's gradient is not wanted. */
+typedef struct gdr_grads {
+  gdr_tensor d_out;       /* in:  [B, H, T, V] bf16, f16 or f32 */
+  const float* d_final;   /* in:  [B, H, K, V] f32 contiguous, or NULL */
+  gdr_tensor d_query;     /* out: [B, H, T, K] */
+  gdr_tensor d_key;       /* out: [B, H, T, K] */
+  gdr_tensor d_value;     /* out: [B, H, T, V] */
+  gdr_tensor d_gate;      /* out: like gate; ptr NULL for DELTANET */
+  gdr_tensor d_beta;      /* out: [B, H, T]; ptr NULL for GLA */
+  float* d_initial;       /* out: [B, H, K, V] f32 contiguous, or NULL */
+} gdr_grads;
+
+/* Chunkwise backward.  Replaces ChunkKimiDeltaAttention.backward (src/ops/kimi_delta_attention.py:560-622:
+ * a forward recompute, then _chunk_intra_backward, _chunk_state_backward, _chunk_backward_dq/_dk,
+ * _chunk_backward_wy_representation, _chunk_backward_kernel_matrix and _chunk_gate_gradient, :200-492) and the
+ * backward of its twins ChunkGatedDeltaNet (gated_deltanet.py:419), ChunkGatedLinearAttention
+ * (gated_linear_attention.py:387) and ChunkDeltaNet (deltanet.py:350).  `args` describes the forward call (its out, ht and
+ * workspace fields are ignored); `grads` names the incoming and outgoing gradients.  `workspace` is device scratch
+ * of gdr_chunk_bwd_workspace_bytes(args) bytes, 256-aligned.  Same limits as gdr_chunk_fwd, except that packed
+ * varlen input (cu_seqlens) is not supported. */
+int gdr_chunk_bwd(const gdr_args* args, const gdr_grads* grads, void* workspace, int64_t workspace_bytes,
+                  hipStream_t stream);
+
+/* Bytes of device workspace gdr_chunk_bwd needs (no pointer dereferenced), or a negative gdr_status.  It holds
+ * the forward record plus the per-chunk states and state gradients (fp32), u and du (bf16) and the fp32
+ * state-side products, the buffers the reference allocates per call (:540-553, :575-606). */
+int64_t gdr_chunk_bwd_workspace_bytes(const gdr_args* args);
 
 /* Recurrent forward (decode).  Replaces the `_recurrent_forward` Triton launch of
  *   recurrent_kimi_delta_attention     src/ops/kimi_delta_attention.py:666-692 (kernel :38-68)

@@ -40,6 +40,8 @@ def test_struct_layout_matches_header(tmp_path):
              'printf("%zu %zu\\n", sizeof(gdr_args), sizeof(gdr_tensor));']
     lines += [f'printf("{f} %zu\\n", offsetof(gdr_args, {f}));' for f in fields]
     lines += [f'printf("t.{f} %zu\\n", offsetof(gdr_tensor, {f}));' for f, _ in lib.GdrTensor._fields_]
+    lines += [f'printf("g.{f} %zu\\n", offsetof(gdr_grads, {f}));' for f, _ in lib.GdrGrads._fields_]
+    lines += ['printf("g.size %zu\\n", sizeof(gdr_grads));']
     lines += ["return 0; }"]
     probe.write_text("\n".join(lines))
     exe = tmp_path / "layout"
@@ -53,6 +55,9 @@ def test_struct_layout_matches_header(tmp_path):
         assert int(offsets[f]) == getattr(lib.GdrArgs, f).offset, f
     for f, _ in lib.GdrTensor._fields_:
         assert int(offsets["t." + f]) == getattr(lib.GdrTensor, f).offset, f
+    for f, _ in lib.GdrGrads._fields_:
+        assert int(offsets["g." + f]) == getattr(lib.GdrGrads, f).offset, f
+    assert int(offsets["g.size"]) == ctypes.sizeof(lib.GdrGrads)
 
 
 def test_last_error_reports_invalid_arguments_without_a_gpu():
@@ -68,6 +73,13 @@ def test_last_error_reports_invalid_arguments_without_a_gpu():
     args.key_dim = 64  # q is NULL
     assert so.gdr_recurrent_fwd(ctypes.byref(args), None) == -1
     assert b"query" in so.gdr_last_error()
+    assert so.gdr_chunk_bwd(ctypes.byref(args), None, None, 0, None) == -1
+    assert b"query" in so.gdr_last_error()
+    # workspace size needs no pointers: B=4, T=4096, H=16, K=V=128
+    args.batch, args.heads, args.seq_len, args.key_dim, args.value_dim = 4, 16, 4096, 128, 128
+    fwd = so.gdr_chunk_workspace_bytes(ctypes.byref(args))
+    bwd = so.gdr_chunk_bwd_workspace_bytes(ctypes.byref(args))
+    assert fwd == 64 * 64 * 71168 and bwd > fwd
 
 
 def _cpu_inputs():
@@ -82,11 +94,15 @@ def test_cpu_tensors_raise_instead_of_falling_back():
         gdr.recurrent_kimi_delta_attention(*_cpu_inputs())
 
 
-def test_gradients_are_refused():
+def test_gradients_refused_where_the_reference_has_no_backward():
+    # the recurrent ops have no backward in the reference either; the chunk backward takes no packed varlen input
     q, k, v, g, b = _cpu_inputs()
     q.requires_grad_()
-    with pytest.raises(NotImplementedError, match="forward-only"):
-        gdr.chunk_kimi_delta_attention(q, k, v, g, b)
+    with pytest.raises(NotImplementedError, match="no backward"):
+        gdr.recurrent_kimi_delta_attention(q, k, v, g, b)
+    cu = torch.tensor([0, q.shape[2]], dtype=torch.int32)
+    with pytest.raises(NotImplementedError, match="varlen"):
+        gdr.chunk_kimi_delta_attention(q, k, v, g, b, cu_seqlens=cu)
 
 
 def test_reference_export_surface():
