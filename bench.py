@@ -11,6 +11,9 @@ One JSON line on stdout:
     source, else null.  mfma_frac reports the same call against the dense bf16 MFMA peak.
   * decode: the batch-256 KDA decode step (fp32 state [256,16,128,128] ~ N(0, 0.02), one token per sequence,
     1000 back-to-back steps, state handed from step to step as the reference API does), in state GB/s.
+  * varlen: the packed-prefill configuration's KDA op (32 sequences, lengths ~U[256, 4096], cu_seqlens).
+  * train: the prefill configuration under torch.autograd, forward then backward (gdr_chunk_bwd), with the
+    backward's algorithmic bytes and HBM fraction.
   * cpu_baseline: the reference's CPU path for the op (fp32 token loop, restated in oracle/) timed on this
     host on a bounded sample of the same prefill workload.
 Only one GPU is used; --gpus above 1 exits with a message.
@@ -159,6 +162,57 @@ def bench_varlen(gdr, workloads, torch, steps, warmup):
             "note": "KDA op only (the layer stack around it is out of scope)"}
 
 
+def train_bytes(B, T, H, K, V, **_):
+    """Algorithmic HBM bytes of one chunk backward: read q, k, v (bf16), gate (fp32), beta, dO (bf16), h0 and the
+    final-state gradient; write dq, dk, dv (bf16), dgate, dbeta (fp32) and dh0."""
+    per_token_head = 3 * K * 2 + V * 2 + K * 4 + 4 + V * 2 + (2 * K + V) * 2 + K * 4 + 4
+    return B * T * H * per_token_head + 3 * B * H * K * V * 4
+
+
+def bench_train(gdr, workloads, torch, steps, warmup):
+    """The prefill configuration's KDA op under torch.autograd: forward with grad, then backward (gdr_chunk_bwd)
+    for q, k, v, gate, beta and the initial state, with a random dO and final-state gradient."""
+    cfg = PREFILL
+    inp = workloads.make_inputs("kda", cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"], seed=0, state_std=0.02,
+                                device="cuda")
+    leaves = [x.detach().clone().requires_grad_() for x in (inp.query, inp.key, inp.value, inp.gate, inp.beta,
+                                                           inp.initial_state)]
+    d_out = torch.randn(inp.value.shape, device="cuda").to(inp.value.dtype)
+    d_final = torch.randn(inp.initial_state.shape, device="cuda")
+
+    def forward():
+        return gdr.chunk_kimi_delta_attention(*leaves[:5], initial_state=leaves[5], output_final_state=True)
+
+    def step():
+        out, final = forward()
+        torch.autograd.backward([out, final], [d_out, d_final])
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    fwd_ms, tot_ms = 0.0, 0.0
+    for _ in range(steps):
+        ev[0].record(stream)
+        out, final = forward()
+        ev[1].record(stream)
+        torch.autograd.backward([out, final], [d_out, d_final])
+        ev[2].record(stream)
+        torch.cuda.synchronize()
+        fwd_ms += ev[0].elapsed_time(ev[1])
+        tot_ms += ev[0].elapsed_time(ev[2])
+    fwd_ms, tot_ms = fwd_ms / steps, tot_ms / steps
+    bwd_ms = tot_ms - fwd_ms
+    tokens = cfg["B"] * cfg["T"]
+    nbytes = train_bytes(**cfg)
+    return {"workload": "kda_chunk_fwd_bwd", "B": cfg["B"], "T": cfg["T"], "H": cfg["H"], "K": cfg["K"],
+            "V": cfg["V"], "ms_forward": round(fwd_ms, 4), "ms_backward": round(bwd_ms, 4),
+            "tokens_per_s_fwd_bwd": round(tokens / (tot_ms * 1e-3), 1),
+            "backward_algorithmic_bytes": nbytes, "backward_gbs": round(nbytes / (bwd_ms * 1e-3) / 1e9, 1),
+            "backward_hbm_frac": round(nbytes / (bwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def cpu_baseline(workloads, torch, budget_s):
     """The reference CPU path (fp32 token loop) on the full prefill workload, repeated until `budget_s`."""
     from oracle import gdr_oracle as oracle
@@ -188,6 +242,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-varlen", action="store_true", help="skip the packed varlen prefill leg")
+    ap.add_argument("--no-train", action="store_true", help="skip the forward + backward (autograd) leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="minimum seconds of CPU baseline work")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the GPU legs, copy a buffer of this many MiB three times (a plain copy kernel of "
@@ -238,6 +293,8 @@ def main():
         record["decode"] = bench_decode(gdr, workloads, torch, warmup=20)
     if not opts.no_varlen:
         record["varlen"] = bench_varlen(gdr, workloads, torch, steps=10, warmup=3)
+    if not opts.no_train:
+        record["train"] = bench_train(gdr, workloads, torch, steps=5, warmup=2)
     if opts.copy_mib:
         src = torch.ones(opts.copy_mib * 2**18, device="cuda")
         dst = torch.empty_like(src)
