@@ -214,9 +214,18 @@ __global__ __launch_bounds__(kDScanThreads, 1) void chunk_dscan_kernel(const gdr
 }
 
 // ================================ state-side products: one workgroup per (chunk, head) ================================
-// All four are products over the value dimension with both operands value-contiguous (16-byte loads straight from
-// global memory / L2 into 16x16x32 MFMA fragments); wave w owns token rows 16 w .. 16 w + 15 of the chunk.
+// Products over the value dimension, wave w owning token rows 16 w .. 16 w + 15 of the chunk:
 //   dqd = dO S^T,  dw = -du S^T,  dkt = u dS'^T  [64][K];   dsc = tril(dO u^T) [64][64];   bnd = rowsum(S (x) dS')
+// S (entering the chunk) and dS' (leaving it) are fp32 in the workspace; 128 value columns at a time are staged
+// once per workgroup into LDS as bf16 MFMA operands, and the fp32 row sums of S (x) dS' are taken on the way.
+// The dO, du and u rows (A operands) come straight from global memory as 16-byte fragments.
+constexpr int kSprodCols = 128;  // value columns staged per pass
+template <int K>
+struct SprodLds {
+  static constexpr int CP = kSprodCols + 8;  // bf16 row pitch
+  static constexpr int SL = 0, DS = K * CP * 2, BYTES = 2 * K * CP * 2;
+};
+
 template <int VARIANT, int K>
 __global__ __launch_bounds__(256) void chunk_sprod_kernel(const gdr_args a, const gdr_grads g, int nc,
                                                           const float* __restrict__ states,
@@ -227,18 +236,20 @@ __global__ __launch_bounds__(256) void chunk_sprod_kernel(const gdr_args a, cons
                                                           float* __restrict__ dsc, float* __restrict__ bnd) {
   constexpr bool kDelta = VARIANT != GDR_GLA;
   constexpr int NT = K / 16;
+  using L = SprodLds<K>;
+  constexpr int CP = L::CP;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __bf16* SL = reinterpret_cast<__bf16*>(smem + L::SL);
+  __bf16* DS = reinterpret_cast<__bf16*>(smem + L::DS);
   const int H = a.heads, V = a.value_dim, len = a.seq_len;
   const int BH = a.batch * H;
   const int bh = blockIdx.x % BH, c = blockIdx.x / BH;
   const int n = bh / H, h = bh % H;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, g4 = lane >> 4;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, l16 = lane & 15, g4 = lane >> 4;
   const size_t kv = size_t(K) * V;
   const float* S = states + (size_t(bh) * (nc + 1) + c) * kv;
   const float* dSn = dstates + (size_t(bh) * (nc + 1) + c + 1) * kv;
-  auto ld8f = [](const float* p) {  // 8 fp32 -> one bf16 MFMA fragment
-    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
-    return bf16x8{bf(a.x), bf(a.y), bf(a.z), bf(a.w), bf(b.x), bf(b.y), bf(b.z), bf(b.w)};
-  };
   const size_t row0 = size_t(bh) * nc * kChunk + c * kChunk;  // first chunk row in ubuf / dubuf / dqd / dw / dkt
   const int t_loc = 16 * wave + l16;
   const int t_glob = c * kChunk + t_loc;
@@ -248,6 +259,49 @@ __global__ __launch_bounds__(256) void chunk_sprod_kernel(const gdr_args a, cons
   const __bf16* ur = ubuf + (row0 + t_loc) * V;
   const __bf16* dur = dubuf + (row0 + t_loc) * V;
   const bf16x8 zero8 = {};
+  // staging assignment: thread -> row d = tid / TPR, a 128 / TPR column run
+  constexpr int TPR = 256 / K, RUN = kSprodCols / TPR;
+  const int sd = tid / TPR, sc0 = (tid % TPR) * RUN;
+  float brow = 0.f;  // partial rowsum(S (x) dS') of row sd
+
+  floatx4 aq[NT], aw[NT], ak[NT], as[4];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) aq[nt] = aw[nt] = ak[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) as[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int vc = 0; vc < V; vc += kSprodCols) {
+    const int cols = min(kSprodCols, V - vc);
+    // stage S and dS' columns [vc, vc + cols) as bf16; fp32 row sums of S (x) dS'
+    for (int x = 0; x < RUN; x += 4) {
+      const int col = sc0 + x;
+      if (col < cols) {
+        const float4 sv = *reinterpret_cast<const float4*>(S + size_t(sd) * V + vc + col);
+        const float4 dv = *reinterpret_cast<const float4*>(dSn + size_t(sd) * V + vc + col);
+        brow += sv.x * dv.x + sv.y * dv.y + sv.z * dv.z + sv.w * dv.w;
+        *reinterpret_cast<bf16x4*>(SL + sd * CP + col) = bf16x4{bf(sv.x), bf(sv.y), bf(sv.z), bf(sv.w)};
+        *reinterpret_cast<bf16x4*>(DS + sd * CP + col) = bf16x4{bf(dv.x), bf(dv.y), bf(dv.z), bf(dv.w)};
+      }
+    }
+    lds_barrier();
+    for (int j0 = 0; j0 < cols; j0 += 32) {
+      const int jj = vc + j0 + 8 * g4;
+      const bf16x8 ado = valid ? ld8(dor + jj) : zero8;
+      const bf16x8 adu = ld8(dur + jj);
+      const bf16x8 au = ld8(ur + jj);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const bf16x8 bs = ld8(SL + (16 * nt + l16) * CP + j0 + 8 * g4);
+        aq[nt] = mfma32(ado, bs, aq[nt]);
+        if constexpr (kDelta) aw[nt] = mfma32(adu, bs, aw[nt]);
+        ak[nt] = mfma32(au, ld8(DS + (16 * nt + l16) * CP + j0 + 8 * g4), ak[nt]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)  // every tile of tril(dO u^T) (the upper ones are discarded): no MFMA under a branch
+        as[j] = mfma32(ado, ld8(ubuf + (row0 + 16 * j + l16) * V + jj), as[j]);
+    }
+    lds_barrier();
+  }
 
   auto store_rows = [&](float* dst, const floatx4* acc, float sign) {
 #pragma unroll
@@ -255,70 +309,23 @@ __global__ __launch_bounds__(256) void chunk_sprod_kernel(const gdr_args a, cons
 #pragma unroll
       for (int r = 0; r < 4; ++r) dst[(row0 + 16 * wave + 4 * g4 + r) * K + 16 * nt + l16] = sign * acc[nt][r];
   };
-
-  // dO S^T and -du S^T share the B fragments (rows of S)
-  {
-    floatx4 aq[NT], aw[NT];
+  store_rows(dqd, aq, 1.f);
+  if constexpr (kDelta) store_rows(dw, aw, -1.f);
+  store_rows(dkt, ak, 1.f);
+  float* d = dsc + (size_t(bh) * nc + c) * kChunk * kChunk;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) aq[nt] = aw[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int j0 = 0; j0 < V; j0 += 32) {
-      const bf16x8 ado = valid ? ld8(dor + j0 + 8 * g4) : zero8;
-      const bf16x8 adu = ld8(dur + j0 + 8 * g4);
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const bf16x8 bs = ld8f(S + size_t(16 * nt + l16) * V + j0 + 8 * g4);
-        aq[nt] = mfma32(ado, bs, aq[nt]);
-        if constexpr (kDelta) aw[nt] = mfma32(adu, bs, aw[nt]);
-      }
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * wave + 4 * g4 + r, s = 16 * j + l16;
+      d[t * kChunk + s] = s <= t ? as[j][r] : 0.f;
     }
-    store_rows(dqd, aq, 1.f);
-    if constexpr (kDelta) store_rows(dw, aw, -1.f);
-  }
-  // u dS'^T
-  {
-    floatx4 ak[NT];
+  if constexpr (VARIANT != GDR_DELTANET) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) ak[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int j0 = 0; j0 < V; j0 += 32) {
-      const bf16x8 au = ld8(ur + j0 + 8 * g4);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) ak[nt] = mfma32(au, ld8f(dSn + size_t(16 * nt + l16) * V + j0 + 8 * g4), ak[nt]);
-    }
-    store_rows(dkt, ak, 1.f);
-  }
-  // tril(dO u^T): tiles (wave, j <= wave); the rest of the 64 x 64 block is written as zeros
-  {
-    floatx4 as[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) as[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int j0 = 0; j0 < V; j0 += 32) {
-      const bf16x8 ado = valid ? ld8(dor + j0 + 8 * g4) : zero8;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)  // every tile (the upper ones are discarded): no MFMA under a branch
-        as[j] = mfma32(ado, ld8(ubuf + (row0 + 16 * j + l16) * V + j0 + 8 * g4), as[j]);
-    }
-    float* d = dsc + (size_t(bh) * nc + c) * kChunk * kChunk;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 16 * wave + 4 * g4 + r, s = 16 * j + l16;
-        d[t * kChunk + s] = s <= t ? as[j][r] : 0.f;
-      }
-  }
-  // rowsum(S (x) dS') per channel, S the state entering the chunk
-  if (VARIANT != GDR_DELTANET && threadIdx.x < K) {
-    const int d = threadIdx.x;
-    float acc = 0.f;
-    for (int j = 0; j < V; j += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(S + size_t(d) * V + j);
-      const float4 y = *reinterpret_cast<const float4*>(dSn + size_t(d) * V + j);
-      acc += x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
-    }
-    bnd[(size_t(bh) * nc + c) * K + d] = acc;
+    for (int m = 1; m < TPR; m <<= 1) brow += __shfl_xor(brow, m);
+    if (tid % TPR == 0) bnd[(size_t(bh) * nc + c) * K + sd] = brow;
   }
 }
-
 
 // =============================== chunk-local gradients: one workgroup per (chunk, head) ===============================
 // LDS (bytes).  Row pitches keep 16-byte alignment and stagger banks.
@@ -353,6 +360,11 @@ struct GradLds {
 constexpr float kDiagSpan = kHotSpan * kLog2e;
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// fp32 16x16x4 MFMA: lane l holds A[l % 16][l / 16] and B[l / 16][l % 16]; D as for the bf16 shapes
+__device__ __forceinline__ floatx4 mfma_f32(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
 __device__ __forceinline__ void store_grad(const gdr_tensor& t, int64_t off, float v) {
   if (t.dtype == GDR_F32) static_cast<float*>(const_cast<void*>(t.ptr))[off] = v;
@@ -513,20 +525,45 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
         for (int r = 0; r < 4; ++r) PP[(16 * p + 4 * g4 + r) * MP + 16 * j + l16] = acc[r];
       }
     }
-    for (int q = lane; q < 120; q += 64) {  // pair (t, s), s < t, of the diagonal tile
-      int t = 1;
-      while (t * (t + 1) / 2 <= q) ++t;
-      const int s = q - t * (t - 1) / 2;
-      const int rt = 16 * p + t, rs = 16 * p + s;
-      float acc = 0.f;
-      for (int d = 0; d < K; d += 4) {
-        const bf16x4 kt4 = ld4(KK + rt * KP + d), ks4 = ld4(KK + rs * KP + d);
-        const float4 bt = *reinterpret_cast<const float4*>(BB + rt * BP + d);
-        const float4 bs = *reinterpret_cast<const float4*>(BB + rs * BP + d);
-        acc += f32(kt4[0]) * f32(ks4[0]) * ex2(bt.x - bs.x) + f32(kt4[1]) * f32(ks4[1]) * ex2(bt.y - bs.y) +
-               f32(kt4[2]) * f32(ks4[2]) * ex2(bt.z - bs.z) + f32(kt4[3]) * f32(ks4[3]) * ex2(bt.w - bs.w);
+    {  // diagonal tile: (k e^{B - m}) (k e^{m - B})^T with m the middle of the block's gate range, so every factor
+       // is within 2^{+-span/2}; channels whose span exceeds kDiagSpan take a zero operand and an exact fp32 sum
+      bf16x8 ae[KS], af[KS];
+      bool any_hot = false;
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const int ch = 32 * kk + 8 * g4;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float top = BB[(16 * p) * BP + ch + j], bot = BB[(16 * p + 15) * BP + ch + j];
+          const bool hot = top - bot > kDiagSpan;
+          any_hot |= hot;
+          const float mid = 0.5f * (top + bot), kv = f32(kraw8[kk][j]);
+          ae[kk][j] = bf(hot ? 0.f : kv * ex2(bl[kk][j] - mid));
+          af[kk][j] = bf(hot ? 0.f : kv * ex2(mid - bl[kk][j]));
+        }
       }
-      PP[rt * MP + rs] = acc;
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) acc = mfma32(ae[kk], af[kk], acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 4 * g4 + r;
+        if (l16 < t) PP[(16 * p + t) * MP + 16 * p + l16] = acc[r];
+      }
+      if (__any(any_hot)) {
+        for (int q = lane; q < 120; q += 64) {  // pair (t, s), s < t: add the hot channels' exact terms
+          int t = 1;
+          while (t * (t + 1) / 2 <= q) ++t;
+          const int s2 = q - t * (t - 1) / 2;
+          const int rt = 16 * p + t, rs = 16 * p + s2;
+          float add = 0.f;
+          for (int d = 0; d < K; ++d) {
+            if (!(BB[(16 * p) * BP + d] - BB[(16 * p + 15) * BP + d] > kDiagSpan)) continue;
+            add += f32(KK[rt * KP + d]) * f32(KK[rs * KP + d]) * ex2(BB[rt * BP + d] - BB[rs * BP + d]);
+          }
+          PP[rt * MP + rs] += add;
+        }
+      }
     }
     for (int idx = lane; idx < 16 * 64; idx += 64) {  // diagonal and everything right of it in this row block
       const int x = idx >> 6, col = idx & 63;
@@ -553,20 +590,25 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
       if (col >= 16 * (p + 1) || col < 16 * p) AA[(16 * p + x) * MP + col] = 0.f;
     }
     lds_barrier();
+    // Block rows 1..3 in turn on fp32 MFMA; wave p owns tile column p:  Y = diag(beta) P[block i, :16i] A[:16i, p],
+    // A_ip = -A_ii Y (zero for p >= i, since A is lower triangular).  Y passes through wave-private scratch in DL.
+#pragma unroll
     for (int i = 1; i < 4; ++i) {
-      const int w = 16 * i;
-      for (int idx = tid; idx < 16 * w; idx += 256) {  // Y = diag(beta) P[block i, :w] A[:w, :w]  -> DL scratch
-        const int x = idx / w, s = idx % w, t = w + x;
-        float acc = 0.f;
-        for (int r = s; r < w; ++r) acc += PP[t * MP + r] * AA[r * MP + s];
-        DL[x * MP + s] = BETA[t] * acc;
-      }
-      lds_barrier();
-      for (int idx = tid; idx < 16 * w; idx += 256) {  // A[block i, :w] = -A_ii Y
-        const int x = idx / w, s = idx % w, t = w + x;
-        float acc = 0.f;
-        for (int xp = 0; xp <= x; ++xp) acc += AA[t * MP + w + xp] * DL[xp * MP + s];
-        AA[t * MP + s] = -acc;
+      const int ta = 16 * i + l16;
+      const float bt = BETA[ta];
+      floatx4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q0 = 0; q0 < 16 * i; q0 += 4)
+        y = mfma_f32(bt * PP[ta * MP + q0 + g4], AA[(q0 + g4) * MP + 16 * p + l16], y);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) DL[(16 * p + 4 * g4 + r) * MP + l16] = y[r];
+      floatx4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q0 = 0; q0 < 16; q0 += 4)
+        z = mfma_f32(AA[ta * MP + 16 * i + q0 + g4], DL[(16 * p + q0 + g4) * MP + l16], z);
+      if (p < i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) AA[(16 * i + 4 * g4 + r) * MP + 16 * p + l16] = -z[r];
       }
       lds_barrier();
     }
@@ -579,6 +621,18 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
       *reinterpret_cast<float4*>(DSC + (idx >> 4) * MP + 4 * (idx & 15)) = src[idx];
   }
   if constexpr (kDelta) {
+    // beta k e^B of this lane's row into the KAP region (free here; KAP is rebuilt after phase 6)
+    {
+      const float bt = BETA[trow];
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        bf16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = bf(f32(kraw8[kk][j]) * bt * ex2(bl[kk][j]));
+        *reinterpret_cast<bf16x8*>(KAP + trow * KP + 32 * kk + 8 * g4) = o;
+      }
+    }
+    lds_barrier();
     floatx4 acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -589,15 +643,8 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
       const float4 w0 = *reinterpret_cast<const float4*>(wr), w1 = *reinterpret_cast<const float4*>(wr + 4);
       const bf16x8 aw = {bf(w0.x), bf(w0.y), bf(w0.z), bf(w0.w), bf(w1.x), bf(w1.y), bf(w1.z), bf(w1.w)};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {  // all four tiles (those right of the diagonal are dropped)
-        const int rs = 16 * j + l16;
-        const bf16x8 ks = *reinterpret_cast<const bf16x8*>(KK + rs * KP + ch);
-        const float bs = BETA[rs];
-        bf16x8 bk;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bk[e] = bf(f32(ks[e]) * bs * ex2(BB[rs * BP + ch + e]));
-        acc[j] = mfma32(aw, bk, acc[j]);
-      }
+      for (int j = 0; j < 4; ++j)  // all four tiles (those right of the diagonal are dropped)
+        acc[j] = mfma32(aw, *reinterpret_cast<const bf16x8*>(KAP + (16 * j + l16) * KP + ch), acc[j]);
     }
     // The value-dimension part accumulates separately and is added after the loop: an MFMA accumulator carried
     // from straight-line code into a loop of runtime trip count came out wrong for K = 64.
@@ -627,31 +674,46 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
 
   // ---- 6. dL = -A^T (dA A^T) on the strict lower triangle; dP = diag(beta) dL; dbeta += rowsum(dL (x) P) ----
   if constexpr (kDelta) {
-    for (int idx = tid; idx < kChunk * kChunk; idx += 256) {  // Z[r][s] = sum_{q <= s} dA[r][q] A[s][q], r > s
-      const int r = idx >> 6, s = idx & 63;
-      float acc = 0.f;
-      if (r > s)
-        for (int q = 0; q <= s; ++q) acc += DL[r * MP + q] * AA[s * MP + q];
-      ZZ[r * MP + s] = acc;
+    // fp32 MFMA (the reference evaluates this product in fp32 too, :458).  Z = dA A^T for row block p, tile columns
+    // si (k over q < 16 (si + 1): A[s][q] = 0 beyond); only Z's strictly lower part reaches dL.
+#pragma unroll
+    for (int si = 0; si < 4; ++si) {
+      floatx4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q0 = 0; q0 < 16 * (si + 1); q0 += 4)
+        z = mfma_f32(DL[(16 * p + l16) * MP + q0 + g4], AA[(16 * si + l16) * MP + q0 + g4], z);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ZZ[(16 * p + 4 * g4 + r) * MP + 16 * si + l16] = z[r];
     }
     lds_barrier();
-    for (int idx = tid; idx < kChunk * kChunk; idx += 256) {
-      const int t = idx >> 6, s = idx & 63;
-      float dp = 0.f;
-      if (t > s) {
-        float acc = 0.f;
-        for (int r = t; r < kChunk; ++r) acc += AA[r * MP + t] * ZZ[r * MP + s];
-        const float dl = -acc;
-        dp = BETA[t] * dl;
-        atomicAdd(DBETA + t, dl * PP[t * MP + s]);
+    // dL = -A^T Z for row block p (k over all r: A[r][t] = 0 for r < t), kept strictly lower; dP = diag(beta) dL
+    float dbr[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int si = 0; si < 4; ++si) {
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r0 = 0; r0 < kChunk; r0 += 4)
+        acc = mfma_f32(AA[(r0 + g4) * MP + 16 * p + l16], ZZ[(r0 + g4) * MP + 16 * si + l16], acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * p + 4 * g4 + r, s = 16 * si + l16;
+        const float dl = t > s ? -acc[r] : 0.f;
+        dbr[r] += dl * PP[t * MP + s];
+        DL[t * MP + s] = BETA[t] * dl;
       }
-      DL[t * MP + s] = dp;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = dbr[r];
+      v += __shfl_xor(v, 1, 16);
+      v += __shfl_xor(v, 2, 16);
+      v += __shfl_xor(v, 4, 16);
+      v += __shfl_xor(v, 8, 16);
+      if (l16 == 0) atomicAdd(DBETA + 16 * p + 4 * g4 + r, v);
     }
     lds_barrier();
-    if constexpr (L::kZAlias) {
-      build_kap();
-      lds_barrier();
-    }
+    build_kap();  // phase 5 (and, when Z aliases it, phase 6) reused the KAP region
+    lds_barrier();
   }
 
   // ---- 7. X1 = A^T dW, X2 = A^T du (rows s of block p): dk += beta e^B X1, dv = beta X2, dbeta ----
@@ -732,6 +794,14 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
   //   left  (rows t of block p, tiles j < p):  e^{B_t - a_{p-1}} sum_j D_pj (k_j e^{a_j - B}) e^{a_{p-1} - a_j}
   //   key   (rows s of block p, tiles i > p):  e^{a_p - B_s} sum_i D_ip^T (x_i e^{B - a_{i-1}}) e^{a_{i-1} - a_p}
   // with D = tril(dO u^T) (dq, and dk with x = q) and D = dP (dk twice, x = k).
+  float pre_qd[NT][4], pre_kt[NT][4];  // assembly operands, loaded here so their latency hides behind phases 8-9
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pre_qd[nt][r] = dqd[(row0 + srow + r) * K + 16 * nt + l16];
+      pre_kt[nt][r] = dkt[(row0 + srow + r) * K + 16 * nt + l16];
+    }
   floatx4 aq[NT], al[NT], ks[NT], kq[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) aq[nt] = al[nt] = ks[nt] = kq[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -911,10 +981,10 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
     for (int r = 0; r < 4; ++r) {
       const int rs = srow + r;
       const float bx = BB[rs * BP + d];
-      const float dq = scale * (dqd[(row0 + rs) * K + d] * ex2(bx) + aq[nt][r]);
+      const float dq = scale * (pre_qd[nt][r] * ex2(bx) + aq[nt][r]);
       const float dkp = dkpos[nt][r] + al[nt][r];
       const float dkn = scale * ks[nt][r] + kq[nt][r];
-      const float dkt_role = dkt[(row0 + rs) * K + d] * ex2(bend[d] - bx);
+      const float dkt_role = pre_kt[nt][r] * ex2(bend[d] - bx);
       const float qv = f32(QQ[rs * KP + d]), kv = f32(KK[rs * KP + d]);
       GT[rs * K + d] = qv * dq + kv * (dkp - dkn);
       KTT[rs * K + d] = kv * dkt_role;
@@ -934,25 +1004,52 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
                      : nullptr;
   const float* bndc = bnd + (size_t(bh) * nc + c) * K;
   if constexpr (kGate == 2) {
-    if (tid < K) {
-      float pre = 0.f;  // KTT -> its exclusive prefix sum
-      for (int t = 0; t < kChunk; ++t) {
-        const float x = KTT[t * K + tid];
-        KTT[t * K + tid] = pre;
-        pre += x;
-      }
-      float acc = bndc[tid] * ex2(bend[tid]);
-      for (int t = kChunk - 1; t >= 0; --t) {
-        acc += GT[t * K + tid];
-        if (t0 + t < len) dgp[int64_t(t0 + t) * g.d_gate.stride_t + tid] = acc + KTT[t * K + tid];
-      }
+    // thread (channel d, half h) scans rows [32 h, 32 h + 32); the halves meet through TOT (free)
+    const int d = tid % K, hh = tid / K;  // K = 128: halves 0, 1; K = 64: quarters 0..3 of 16 rows
+    constexpr int NPART = 256 / K, RP = kChunk / NPART;
+    float gtv[RP], ktv[RP];
+#pragma unroll
+    for (int x = 0; x < RP; ++x) {
+      gtv[x] = GT[(RP * hh + x) * K + d];
+      ktv[x] = KTT[(RP * hh + x) * K + d];
+    }
+    float gsum = 0.f, ksum = 0.f;
+#pragma unroll
+    for (int x = 0; x < RP; ++x) gsum += gtv[x], ksum += ktv[x];
+    TOT[hh * K + d] = gsum;  // TOT holds 4 K floats: part sums of GT, then of KTT in the second half
+    lds_barrier();
+    float gafter = bndc[d] * ex2(bend[d]), kbefore = 0.f;  // GT after this part, KTT before it
+    for (int o = hh + 1; o < NPART; ++o) gafter += TOT[o * K + d];
+    lds_barrier();
+    TOT[hh * K + d] = ksum;
+    lds_barrier();
+    for (int o = 0; o < hh; ++o) kbefore += TOT[o * K + d];
+    float suf = gafter, pre = kbefore;
+    float kex[RP];
+#pragma unroll
+    for (int x = 0; x < RP; ++x) {
+      kex[x] = pre;
+      pre += ktv[x];
+    }
+#pragma unroll
+    for (int x = RP - 1; x >= 0; --x) {
+      suf += gtv[x];
+      const int t = RP * hh + x;
+      if (t0 + t < len) dgp[int64_t(t0 + t) * g.d_gate.stride_t + d] = suf + kex[x];
     }
   } else if constexpr (kGate == 1) {
-    if (tid < kChunk) {  // per-row sums over the channels into TOT (free): [0, 64) of GT, [64, 128) of KTT
+    // per-row sums over the channels into TOT (free): [0, 64) of GT, [64, 128) of KTT; wave w sums rows
+    // 16 w .. 16 w + 15 with lanes over channels
+    for (int x = 0; x < 16; ++x) {
+      const int t = 16 * p + x;
       float a = 0.f, b = 0.f;
-      for (int d = 0; d < K; ++d) a += GT[tid * K + d], b += KTT[tid * K + d];
-      TOT[tid] = a;
-      TOT[kChunk + tid] = b;
+      for (int d = lane; d < K; d += 64) a += GT[t * K + d], b += KTT[t * K + d];
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) a += __shfl_xor(a, m), b += __shfl_xor(b, m);
+      if (lane == 0) {
+        TOT[t] = a;
+        TOT[kChunk + t] = b;
+      }
     }
     lds_barrier();
     if (tid == 0) {
@@ -995,6 +1092,9 @@ hipError_t launch_bwd_typed(const gdr_args& a, const gdr_grads& g, const BwdLayo
     if (e == hipSuccess)
       e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_grad_kernel<VARIANT, K>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, grad_lds);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_sprod_kernel<VARIANT, K>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, SprodLds<K>::BYTES);
     if (e != hipSuccess) return e;
     configured = true;
   }
@@ -1012,8 +1112,8 @@ hipError_t launch_bwd_typed(const gdr_args& a, const gdr_grads& g, const BwdLayo
   const int xcd_map = (bh % 8 == 0) ? 1 : 0;
   hipLaunchKernelGGL((chunk_dscan_kernel<VARIANT, K>), dim3(bh * n_slices), dim3(kDScanThreads), dscan_lds, stream,
                      a, g, n_slices, xcd_map, nc, rec, ws + Lw.rec, dstates, dubuf);
-  hipLaunchKernelGGL((chunk_sprod_kernel<VARIANT, K>), dim3(bh * nc), dim3(256), 0, stream, a, g, nc, states,
-                     dstates, ubuf, dubuf, dqd, dw, dkt, dsc, bnd);
+  hipLaunchKernelGGL((chunk_sprod_kernel<VARIANT, K>), dim3(bh * nc), dim3(256), SprodLds<K>::BYTES, stream, a, g,
+                     nc, states, dstates, ubuf, dubuf, dqd, dw, dkt, dsc, bnd);
   hipLaunchKernelGGL((chunk_grad_kernel<VARIANT, K>), dim3(bh * nc), dim3(256), grad_lds, stream, a, g, nc, dqd, dw,
                      dkt, dsc, bnd, dubuf);
   return hipGetLastError();
