@@ -674,7 +674,7 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
 
   // ---- 6. dL = -A^T (dA A^T) on the strict lower triangle; dP = diag(beta) dL; dbeta += rowsum(dL (x) P) ----
   if constexpr (kDelta) {
-    // fp32 MFMA (the reference evaluates this product in fp32 too, :458).  Z = dA A^T for row block p, tile columns
+    // fp32 MFMA (the reference evaluates this product in fp32 too, kimi_delta_attention.py:385).  Z = dA A^T for row block p, tile columns
     // si (k over q < 16 (si + 1): A[s][q] = 0 beyond); only Z's strictly lower part reaches dL.
 #pragma unroll
     for (int si = 0; si < 4; ++si) {
