@@ -442,6 +442,11 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
     }
   }
   if (g4 == 0) BETA[trow] = (kDelta && valid) ? betap[int64_t(tc) * a.beta.stride_t] : 0.f;
+  {  // tril(dO u^T) into LDS now (its region is free until phase 5) so the load overlaps phases 1-4
+    const float4* src = reinterpret_cast<const float4*>(dsc + (size_t(bh) * nc + c) * kChunk * kChunk);
+    for (int idx = tid; idx < kChunk * kChunk / 4; idx += 256)
+      *reinterpret_cast<float4*>(DSC + (idx >> 4) * MP + 4 * (idx & 15)) = src[idx];
+  }
   if (tid < 64) DBETA[tid] = 0.f;
   {
     const float kf = valid ? kLog2e : 0.f;
@@ -614,12 +619,7 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
     }
   }
 
-  // ---- 5. tril(dO u^T) into LDS; dA = dW (beta K e^B)^T + du (beta V)^T, tiles (p, j <= p) ----
-  {
-    const float4* src = reinterpret_cast<const float4*>(dsc + (size_t(bh) * nc + c) * kChunk * kChunk);
-    for (int idx = tid; idx < kChunk * kChunk / 4; idx += 256)
-      *reinterpret_cast<float4*>(DSC + (idx >> 4) * MP + 4 * (idx & 15)) = src[idx];
-  }
+  // ---- 5. dA = dW (beta K e^B)^T + du (beta V)^T, tiles (p, j <= p) ----
   if constexpr (kDelta) {
     // beta k e^B of this lane's row into the KAP region (free here; KAP is rebuilt after phase 6)
     {
@@ -712,8 +712,6 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
       if (l16 == 0) atomicAdd(DBETA + 16 * p + 4 * g4 + r, v);
     }
     lds_barrier();
-    build_kap();  // phase 5 (and, when Z aliases it, phase 6) reused the KAP region
-    lds_barrier();
   }
 
   // ---- 7. X1 = A^T dW, X2 = A^T du (rows s of block p): dk += beta e^B X1, dv = beta X2, dbeta ----
@@ -721,6 +719,7 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) dkpos[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
   const int srow = 16 * p + 4 * g4;  // this lane's accumulator rows srow + r
+  auto tr_off = [&](int base, int row, int col) { return base + 2 * (row * KP + col); };
   if constexpr (kDelta) {
     bf16x4 at[4];  // (A^T)[16 p + l16][16 kb + 4 g4 + r]; zero for kb < p (A is lower triangular)
 #pragma unroll
@@ -730,18 +729,26 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
       for (int r = 0; r < 4; ++r) v[r] = AA[(16 * kb + 4 * g4 + r) * MP + 16 * p + l16];
       at[kb] = pack4(v);
     }
+    lds_barrier();  // A lives in registers now; P is dead: AA and PP take staged operands
+    // dW as bf16 [64][KP] in PP, read by the transposing LDS read as the B operand of X1 = A^T dW
+    __bf16* WS = reinterpret_cast<__bf16*>(smem + L::PP);
+    __bf16* US = reinterpret_cast<__bf16*>(smem + L::KAP);  // du columns of one pass (KAP is rebuilt afterwards)
+    __bf16* VS = reinterpret_cast<__bf16*>(smem + L::AA);   // v columns of one pass
+    for (int idx = tid; idx < kChunk * K / 4; idx += 256) {
+      const int row = idx / (K / 4), col = 4 * (idx % (K / 4));
+      const float4 w = *reinterpret_cast<const float4*>(dwt + (row0 + row) * K + col);
+      *reinterpret_cast<bf16x4*>(WS + row * KP + col) = bf16x4{bf(w.x), bf(w.y), bf(w.z), bf(w.w)};
+    }
+    lds_barrier();
     float dbp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int d = 16 * nt + l16;
       floatx4 x1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        floatx4 bw;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) bw[r] = dwt[(row0 + 16 * kb + 4 * g4 + r) * K + d];
-        x1 = mfma16(at[kb], pack4(bw), x1);
-      }
+      for (int kb = 0; kb < 4; ++kb)
+        x1 = mfma16(at[kb], lds_read_tr(smem, tr_off(L::PP, 16 * kb + 4 * g4 + (l16 >> 2), 16 * nt + 4 * (l16 & 3))),
+                    x1);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int rs = srow + r;
@@ -750,26 +757,35 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
         dbp[r] += x1[r] * f32(KK[rs * KP + d]) * eb;
       }
     }
-    for (int j0 = 0; j0 < V; j0 += 16) {
-      const int jc = j0 + l16;
-      floatx4 x2 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        floatx4 bu;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) bu[r] = f32(dubuf[(row0 + 16 * kb + 4 * g4 + r) * V + jc]);
-        x2 = mfma16(at[kb], pack4(bu), x2);
+    // X2 = A^T du in passes of K value columns: du and v staged as bf16 (16-byte global loads)
+    for (int vc = 0; vc < V; vc += K) {
+      const int cols = min(K, V - vc);
+      for (int idx = tid; idx < kChunk * cols / 8; idx += 256) {
+        const int row = idx / (cols / 8), col = 8 * (idx % (cols / 8));
+        *reinterpret_cast<bf16x8*>(US + row * KP + col) = ld8(dubuf + (row0 + row) * V + vc + col);
+        *reinterpret_cast<bf16x8*>(VS + row * KP + col) =
+            ld8(vp + int64_t(min(t0 + row, len - 1)) * a.v.stride_t + vc + col);
       }
+      lds_barrier();
+      for (int j0 = 0; j0 < cols; j0 += 16) {
+        const int jc = vc + j0 + l16;
+        floatx4 x2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int rs = srow + r;
-        if (t0 + rs < len) {
-          const int64_t tt = t0 + rs;
-          store_grad(g.d_value, n * g.d_value.stride_b + h * g.d_value.stride_h + tt * g.d_value.stride_t + jc,
-                     BETA[rs] * x2[r]);
-          dbp[r] += x2[r] * f32(vp[tt * a.v.stride_t + jc]);
+        for (int kb = 0; kb < 4; ++kb)
+          x2 = mfma16(at[kb], lds_read_tr(smem, tr_off(L::KAP, 16 * kb + 4 * g4 + (l16 >> 2), j0 + 4 * (l16 & 3))),
+                      x2);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int rs = srow + r;
+          if (t0 + rs < len) {
+            const int64_t tt = t0 + rs;
+            store_grad(g.d_value, n * g.d_value.stride_b + h * g.d_value.stride_h + tt * g.d_value.stride_t + jc,
+                       BETA[rs] * x2[r]);
+            dbp[r] += x2[r] * f32(VS[rs * KP + j0 + l16]);
+          }
         }
       }
+      lds_barrier();
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -780,6 +796,8 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
       v += __shfl_xor(v, 8, 16);
       if (l16 == 0) atomicAdd(DBETA + srow + r, v);
     }
+    build_kap();  // phases 5-7 reused the KAP region
+    lds_barrier();
   } else {
     for (int idx = tid; idx < kChunk * V; idx += 256) {  // GLA: U = V, so dv = du
       const int rr = idx / V, jc = idx % V;
@@ -805,7 +823,6 @@ __global__ __launch_bounds__(256, 1) void chunk_grad_kernel(const gdr_args a, co
   floatx4 aq[NT], al[NT], ks[NT], kq[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) aq[nt] = al[nt] = ks[nt] = kq[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  auto tr_off = [&](int base, int row, int col) { return base + 2 * (row * KP + col); };
   // Both loops run over every tile with zero operands outside the range: no MFMA sits under a branch.
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
