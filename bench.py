@@ -12,6 +12,9 @@ One JSON line on stdout:
   * decode: the batch-256 KDA decode step (fp32 state [256,16,128,128] ~ N(0, 0.02), one token per sequence,
     1000 back-to-back steps, state handed from step to step as the reference API does), in state GB/s.
   * varlen: the packed-prefill configuration's KDA op (32 sequences, lengths ~U[256, 4096], cu_seqlens).
+  * verify: a speculative-decoding cycle at the decode configuration's state size (batch 256, 16 heads, 128 x 128
+    fp32 state) on 8-token blocks: verify (gdr_recurrent_verify, no final state) then commit of a per-sequence
+    accepted prefix drawn on the device (gdr_recurrent_commit), in algorithmic GB/s per kernel and per cycle.
   * train: the prefill configuration under torch.autograd, forward then backward (gdr_chunk_bwd), with the
     backward's algorithmic bytes and HBM fraction.
   * cpu_baseline: the reference's CPU path for the op (fp32 token loop, restated in oracle/) timed on this
@@ -36,6 +39,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PREFILL = dict(B=4, T=4096, H=16, K=128, V=128, chunk=64)
 DECODE = dict(B=256, H=16, K=128, V=128, steps=1000)
+VERIFY = dict(B=256, H=16, K=128, V=128, T=8, cycles=200)
 VARLEN = dict(n_seqs=32, low=256, high=4096, H=16, K=128, V=128)
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 
@@ -130,6 +134,70 @@ def bench_decode(gdr, workloads, torch, warmup):
             "unit": "GB/s (state + io bytes per step)", "tokens_per_s": round(cfg["B"] / (ms * 1e-3), 1),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": committed_traffic("recurrent_kda_decode")}}
+
+
+def verify_bytes(B, H, K, V, T, **_):
+    """Algorithmic bytes of one verify call: the state read once; q, k, v, gate, beta read and out written per
+    token; the fp32 update record written."""
+    bf16, f32 = 2, 4
+    io = B * H * T * (2 * K * bf16 + V * bf16 + K * f32 + f32 + V * bf16)
+    return B * H * K * V * f32 + io + B * H * T * V * f32
+
+
+def commit_bytes(accepted_tokens, B, H, K, V, **_):
+    """Algorithmic bytes of one commit: the state read and written once, and k (bf16), the gate and the record row
+    of each accepted token (accepted_tokens summed over the batch)."""
+    bf16, f32 = 2, 4
+    return 2 * B * H * K * V * f32 + accepted_tokens * H * (K * bf16 + K * f32 + V * f32)
+
+
+def bench_verify(gdr, workloads, torch, warmup):
+    cfg = VERIFY
+    dev = torch.device("cuda")
+    B, H, K, V, T = cfg["B"], cfg["H"], cfg["K"], cfg["V"], cfg["T"]
+    ring = [workloads.make_inputs("kda", B, T, H, K, V, seed=200 + i, device=dev) for i in range(8)]
+    gen = torch.Generator("cpu").manual_seed(3)
+    counts = [torch.randint(0, T + 1, (B,), generator=gen, dtype=torch.int32) for _ in range(8)]
+    accepted = [c.to(dev) for c in counts]
+    state = workloads.decode_state(B, H, K, V, std=0.02, seed=9, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def timed(fn, n):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(n):
+            fn(i)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / n
+
+    with torch.no_grad():
+        blocks = [gdr.verify_kimi_delta_attention(*r.args(), initial_state=state)[2] for r in ring]
+        verify_only = lambda i: gdr.verify_kimi_delta_attention(*ring[i % 8].args(), initial_state=state)
+        commit_only = lambda i: blocks[i % 8].commit(accepted[i % 8])
+        cur = [state]
+
+        def cycle(i):
+            _, _, block = gdr.verify_kimi_delta_attention(*ring[i % 8].args(), initial_state=cur[0])
+            cur[0] = block.commit(accepted[i % 8])
+
+        for fn in (verify_only, commit_only, cycle):
+            for i in range(warmup):
+                fn(i)
+        torch.cuda.synchronize()
+        v_ms = timed(verify_only, cfg["cycles"])
+        c_ms = timed(commit_only, cfg["cycles"])
+        y_ms = timed(cycle, cfg["cycles"])
+    mean_accepted = sum(int(c.sum()) for c in counts) / len(counts)
+    vb, cb = verify_bytes(**cfg), commit_bytes(mean_accepted, **cfg)
+    gbs = lambda nbytes, ms: nbytes / (ms * 1e-3) / 1e9
+    return {"workload": "kda_verify_commit", "B": B, "H": H, "K": K, "V": V, "T": T, "cycles": cfg["cycles"],
+            "mean_accepted_tokens": round(mean_accepted / B, 3),
+            "us_verify": round(v_ms * 1e3, 2), "us_commit": round(c_ms * 1e3, 2), "us_cycle": round(y_ms * 1e3, 2),
+            "verify_gbs": round(gbs(vb, v_ms), 1), "commit_gbs": round(gbs(cb, c_ms), 1),
+            "accepted_tokens_per_s": round(mean_accepted / (y_ms * 1e-3), 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs(vb + cb, y_ms), 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs(vb + cb, y_ms) / HBM_PEAK_GBS, 4)}}
 
 
 def bench_varlen(gdr, workloads, torch, steps, warmup):
@@ -241,6 +309,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-verify", action="store_true", help="skip the speculative verify + commit leg")
     ap.add_argument("--no-varlen", action="store_true", help="skip the packed varlen prefill leg")
     ap.add_argument("--no-train", action="store_true", help="skip the forward + backward (autograd) leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="minimum seconds of CPU baseline work")
@@ -291,6 +360,8 @@ def main():
     }
     if not opts.no_decode:
         record["decode"] = bench_decode(gdr, workloads, torch, warmup=20)
+    if not opts.no_verify:
+        record["verify"] = bench_verify(gdr, workloads, torch, warmup=10)
     if not opts.no_varlen:
         record["varlen"] = bench_varlen(gdr, workloads, torch, steps=10, warmup=3)
     if not opts.no_train:

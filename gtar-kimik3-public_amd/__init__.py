@@ -2,14 +2,17 @@
 
 The export surface mirrors the reference's op package for this family (src/ops/__init__.py:1-6): a
 `chunk_*` (prefill) and a `recurrent_*` (decode) function per variant, backed by the hand-written gfx950 HIP
-kernels of libgdr.so.  `RecurrentCache` mirrors the decode-state owner of src/cache.py:48-86.
+kernels of libgdr.so.  `RecurrentCache` mirrors the decode-state owner of src/cache.py:48-86.  A `verify_*`
+function per variant serves speculative decoding (the verify / accept cycle of src/speculative.py:344-449).
 """
 
 from .cache import RecurrentCache
-from .deltanet import chunk_deltanet, recurrent_deltanet
-from .gated_deltanet import chunk_gated_deltanet, recurrent_gated_deltanet
-from .gated_linear_attention import chunk_gated_linear_attention, recurrent_gated_linear_attention
-from .kimi_delta_attention import chunk_kimi_delta_attention, recurrent_kimi_delta_attention
+from .deltanet import chunk_deltanet, recurrent_deltanet, verify_deltanet
+from .gated_deltanet import chunk_gated_deltanet, recurrent_gated_deltanet, verify_gated_deltanet
+from .gated_linear_attention import (chunk_gated_linear_attention, recurrent_gated_linear_attention,
+                                     verify_gated_linear_attention)
+from .kimi_delta_attention import chunk_kimi_delta_attention, recurrent_kimi_delta_attention, verify_kimi_delta_attention
+from .verify import VerifiedBlock
 
 __all__ = [
     "RecurrentCache",
@@ -21,4 +24,9 @@ __all__ = [
     "recurrent_gated_deltanet",
     "recurrent_gated_linear_attention",
     "recurrent_kimi_delta_attention",
+    "VerifiedBlock",
+    "verify_deltanet",
+    "verify_gated_deltanet",
+    "verify_gated_linear_attention",
+    "verify_kimi_delta_attention",
 ]

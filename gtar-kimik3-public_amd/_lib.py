@@ -18,7 +18,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.join(_HERE, "libgdr.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 KDA, GDN, GLA, DELTANET = 0, 1, 2, 3
 F32, BF16, F16 = 0, 1, 2
@@ -83,6 +83,9 @@ EXPORTS = {
     "gdr_chunk_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
     "gdr_chunk_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(GdrArgs)]),
     "gdr_recurrent_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
+    "gdr_recurrent_verify": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p]),
+    "gdr_recurrent_commit": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_void_p]),
     "gdr_last_error": (ctypes.c_char_p, []),
     "gdr_abi_version": (ctypes.c_int, []),
 }
@@ -195,3 +198,25 @@ def chunk_backward(args: GdrArgs, grads: GdrGrads, device: torch.device) -> None
                            ctypes.c_int64(int(nbytes)), ctypes.c_void_p(stream))
     if rc != 0:
         raise RuntimeError(f"gdr_chunk_bwd failed ({rc}): {lib.gdr_last_error().decode()}")
+
+
+def _check(entry: str, rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{entry} failed ({rc}): {load_library().gdr_last_error().decode()}")
+
+
+def verify(args: GdrArgs, updates: torch.Tensor, device: torch.device) -> None:
+    """Enqueue gdr_recurrent_verify on torch's current stream; `updates` is the f32 [B, H, T, V] record."""
+    lib = load_library()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    _check("gdr_recurrent_verify", lib.gdr_recurrent_verify(ctypes.byref(args), ctypes.c_void_p(updates.data_ptr()),
+                                                            ctypes.c_void_p(stream)))
+
+
+def commit(args: GdrArgs, updates: torch.Tensor, accepted: torch.Tensor | None, device: torch.device) -> None:
+    """Enqueue gdr_recurrent_commit; `accepted` is a device int32 [B] tensor or None (all tokens)."""
+    lib = load_library()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    acc = ctypes.c_void_p(accepted.data_ptr()) if accepted is not None else None
+    _check("gdr_recurrent_commit", lib.gdr_recurrent_commit(ctypes.byref(args), ctypes.c_void_p(updates.data_ptr()),
+                                                            acc, ctypes.c_void_p(stream)))

@@ -103,6 +103,39 @@ int gdr_recurrent_fwd(const gdr_args* a, hipStream_t stream) {
   return GDR_OK;
 }
 
+int gdr_recurrent_verify(const gdr_args* a, float* updates, hipStream_t stream) {
+  int rc = check_common(a, false);
+  if (rc) return rc;
+  if (a->q.dtype != a->k.dtype || a->q.dtype != a->v.dtype || a->q.dtype == GDR_F16)
+    return fail(GDR_ERR_UNSUPPORTED, "recurrent mode reads q, k, v of one dtype, bf16 or f32 (got dtype codes %d, %d, %d)",
+                a->q.dtype, a->k.dtype, a->v.dtype);
+  if (!updates) return fail(GDR_ERR_INVALID, "updates: null pointer");
+  if (reinterpret_cast<uintptr_t>(updates) % 16) return fail(GDR_ERR_INVALID, "updates must be 16-byte aligned");
+  hipError_t e = gdr::launch_verify(*a, updates, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "verify launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
+int gdr_recurrent_commit(const gdr_args* a, const float* updates, const int32_t* accepted, hipStream_t stream) {
+  int rc = check_shape(a, false);
+  if (rc) return rc;
+  const bool has_gate = a->variant != GDR_DELTANET;
+  if ((rc = check_view(a->k, "key", true, false))) return rc;
+  if (a->k.dtype == GDR_F16) return fail(GDR_ERR_UNSUPPORTED, "key: bf16 or f32 only");
+  if ((rc = check_view(a->gate, "gate", has_gate, true))) return rc;
+  if (!has_gate && a->gate.ptr) return fail(GDR_ERR_INVALID, "DeltaNet takes no gate");
+  if (!a->ht) return fail(GDR_ERR_INVALID, "ht: null pointer (the commit writes the state)");
+  if (!updates) return fail(GDR_ERR_INVALID, "updates: null pointer");
+  if ((reinterpret_cast<uintptr_t>(a->h0) | reinterpret_cast<uintptr_t>(a->ht) |
+       reinterpret_cast<uintptr_t>(updates)) % 16 != 0)
+    return fail(GDR_ERR_INVALID, "initial/final state and updates must be 16-byte aligned");
+  hipError_t e = gdr::launch_commit(*a, updates, accepted, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "commit launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
 int64_t gdr_chunk_workspace_bytes(const gdr_args* a) {
   const int rc = check_shape(a, true);
   if (rc) return rc;

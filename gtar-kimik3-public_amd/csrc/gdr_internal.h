@@ -10,6 +10,13 @@ namespace gdr {
 // Enqueue the recurrent forward; `a` has been validated.
 hipError_t launch_recurrent(const gdr_args& a, hipStream_t stream);
 
+// The recurrent forward that also records each token's update row u_t, fp32 [B, H, T, V], into `updates`.
+hipError_t launch_verify(const gdr_args& a, float* updates, hipStream_t stream);
+
+// a.ht <- the state after the first clamp(accepted[b], 0, T) tokens (all T when accepted is NULL), rebuilt from
+// a.h0, k, the gate and a verify record.
+hipError_t launch_commit(const gdr_args& a, const float* updates, const int32_t* accepted, hipStream_t stream);
+
 // Enqueue the chunkwise forward; `a` has been validated (q, k, v share one dtype).
 hipError_t launch_chunk(const gdr_args& a, hipStream_t stream);
 

@@ -12,6 +12,7 @@ import torch
 
 from . import _lib
 from ._common import run
+from .verify import verify
 
 
 @torch.compiler.disable
@@ -41,3 +42,17 @@ def recurrent_deltanet(
 ):
     """Token-by-token (decode) DeltaNet forward."""
     return run(_lib.DELTANET, False, query, key, value, None, beta, scale, initial_state, output_final_state)
+
+
+def verify_deltanet(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+):
+    """Speculative-decoding verify over a block of tokens: the recurrent forward plus a `VerifiedBlock` whose
+    `commit(accepted)` rebuilds the state after any accepted prefix.  Returns `(out, final_state or None, block)`."""
+    return verify(_lib.DELTANET, query, key, value, None, beta, scale, initial_state, output_final_state)

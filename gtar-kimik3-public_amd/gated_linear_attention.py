@@ -12,6 +12,7 @@ import torch
 
 from . import _lib
 from ._common import run
+from .verify import verify
 
 
 @torch.compiler.disable
@@ -40,3 +41,17 @@ def recurrent_gated_linear_attention(
 ):
     """Token-by-token (decode) GLA forward."""
     return run(_lib.GLA, False, query, key, value, gate, None, scale, initial_state, output_final_state)
+
+
+def verify_gated_linear_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    gate: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+):
+    """Speculative-decoding verify over a block of tokens: the recurrent forward plus a `VerifiedBlock` whose
+    `commit(accepted)` rebuilds the state after any accepted prefix.  Returns `(out, final_state or None, block)`."""
+    return verify(_lib.GLA, query, key, value, gate, None, scale, initial_state, output_final_state)

@@ -14,6 +14,7 @@ import torch
 
 from . import _lib
 from ._common import run
+from .verify import verify
 
 
 @torch.compiler.disable
@@ -45,3 +46,18 @@ def recurrent_kimi_delta_attention(
 ):
     """Token-by-token (decode) KDA forward; the state stays in registers for all T tokens."""
     return run(_lib.KDA, False, query, key, value, gate, beta, scale, initial_state, output_final_state)
+
+
+def verify_kimi_delta_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    gate: torch.Tensor,
+    beta: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+):
+    """Speculative-decoding verify over a block of tokens: the recurrent forward plus a `VerifiedBlock` whose
+    `commit(accepted)` rebuilds the state after any accepted prefix.  Returns `(out, final_state or None, block)`."""
+    return verify(_lib.KDA, query, key, value, gate, beta, scale, initial_state, output_final_state)

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GDR_ABI_VERSION 3
+#define GDR_ABI_VERSION 4
 
 typedef enum gdr_variant { GDR_KDA = 0, GDR_GDN = 1, GDR_GLA = 2, GDR_DELTANET = 3 } gdr_variant;
 
@@ -135,6 +135,26 @@ int64_t gdr_chunk_bwd_workspace_bytes(const gdr_args* args);
  * q, k, v must share one dtype, bf16 or f32 (the Python layer widens mixed or f16 inputs to f32, exactly); out may
  * be bf16, f16 or f32.  Supports K in {64, 128}, V a multiple of 32, any T >= 1 (cu_seqlens must be NULL). */
 int gdr_recurrent_fwd(const gdr_args* args, hipStream_t stream);
+
+/* Multi-token verify for speculative decoding: gdr_recurrent_fwd over a block of T tokens (the pending token plus
+ * the drafts) that also records each token's state update row u_t (the row added to the state as k_t^T u_t:
+ * beta_t (v_t - k_t S_t) for the delta-rule variants, v_t for GLA) into `updates`, f32 [B, H, T, V] contiguous,
+ * 16-byte aligned.  With that record gdr_recurrent_commit rebuilds the state after any accepted prefix from the
+ * state the block started from, so nothing is cloned before the verify and nothing is replayed after a rejection.
+ * Replaces the verify forward of SpeculativeEngine.generate (src/speculative.py:351-356: RecurrentCache.fork, then
+ * the chunk op on the block, padded to 64 tokens by src/ops/utils.py:70-72).  args->ht may be NULL or receive the
+ * state after all T tokens.  Same dtype rules and limits as gdr_recurrent_fwd. */
+int gdr_recurrent_verify(const gdr_args* args, float* updates, hipStream_t stream);
+
+/* State after the first n_b = clamp(accepted[b], 0, T) tokens of a verified block, for each sequence b:
+ *     S = h0 (zero when NULL);  for t < n_b:  S = diag(e^{g_t}) S + k_t^T updates[b, :, t]
+ * (scalar decay for GDN, none for DeltaNet).  Reads the variant, sizes, k (bf16 or f32), gate and h0 of `args` and
+ * writes args->ht (required; may alias h0); q, v, beta, out and scale are ignored.  `accepted` is a device int32 [B]
+ * array, or NULL for all T tokens, so an accept count decided on the device never has to reach the host.  With
+ * the inputs of the verify call, accepted = T reproduces the final state gdr_recurrent_verify writes bit for bit.
+ * Replaces RecurrentCache.commit / rollback plus the replay forward of the accepted prefix
+ * (src/cache.py:59-86, src/speculative.py:397, 425-449). */
+int gdr_recurrent_commit(const gdr_args* args, const float* updates, const int32_t* accepted, hipStream_t stream);
 
 /* Thread-local description of the calling thread's last failure ("" if none).  No reference counterpart:
  * the reference surfaces failures as Python exceptions raised by Triton. */

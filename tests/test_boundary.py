@@ -132,3 +132,51 @@ def test_recurrent_cache_fork_rollback_restores_state():
     assert torch.count_nonzero(cache.conv_states[0]) == 0
     with pytest.raises(RuntimeError):
         cache.commit(1)
+
+
+def test_verify_and_commit_reject_bad_arguments_without_a_gpu():
+    so = lib.load_library()
+    args = lib.GdrArgs()
+    args.abi_version = lib.ABI_VERSION
+    args.variant, args.batch, args.heads, args.seq_len, args.key_dim, args.value_dim = 0, 1, 1, 4, 64, 64
+    assert so.gdr_recurrent_verify(ctypes.byref(args), None, None) == -1
+    assert b"query" in so.gdr_last_error()
+    assert so.gdr_recurrent_commit(ctypes.byref(args), None, None, None) == -1
+    assert b"key" in so.gdr_last_error()
+    args.k.ptr, args.k.dtype = 256, lib.BF16  # never dereferenced: validation stops before any launch
+    args.gate.ptr, args.gate.dtype = 512, lib.F32
+    assert so.gdr_recurrent_commit(ctypes.byref(args), 1024, None, None) == -1
+    assert b"ht" in so.gdr_last_error()
+    args.ht = 2048
+    assert so.gdr_recurrent_commit(ctypes.byref(args), None, None, None) == -1
+    assert b"updates" in so.gdr_last_error()
+    assert so.gdr_recurrent_commit(ctypes.byref(args), 1028, None, None) == -1
+    assert b"aligned" in so.gdr_last_error()
+
+
+class _FakeBlock:
+    """Stands in for a VerifiedBlock on the CPU: commit(n) returns a recognisable state."""
+
+    def __init__(self, initial_state):
+        self.initial_state = initial_state
+
+    def commit(self, n):
+        return self.initial_state + n
+
+
+def test_recurrent_cache_accept_adopts_the_prefix_state():
+    cache = gdr.RecurrentCache(1, 2, 4, 4, 8, 4, "cpu", torch.float32)
+    cache.update(torch.randn(1, 2, 4, 4), 5)
+    forked = cache.state
+    with pytest.raises(RuntimeError):
+        cache.accept(1, _FakeBlock(forked))
+    cache.fork()
+    assert cache._snapshot[0] is forked  # held by reference, not cloned
+    with pytest.raises(ValueError, match="fork"):
+        cache.accept(2, _FakeBlock(forked.clone()))
+    tails = [torch.full_like(c, 3.0) for c in cache.conv_states]
+    state = cache.accept(2, _FakeBlock(forked), tails)
+    assert torch.equal(state, forked + 2) and cache.state is state and cache.seq_len == 7
+    assert all(torch.equal(c, t) for c, t in zip(cache.conv_states, tails))
+    with pytest.raises(RuntimeError):
+        cache.rollback()
