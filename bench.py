@@ -69,16 +69,16 @@ def source_hash(source):
     return hashlib.sha256(open(path, "rb").read()).hexdigest()[:16]
 
 
-def committed_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, or None
-    when the summary was taken on a different revision of the kernel's source file."""
+def committed_traffic(workload):
+    """HBM bytes per call of `workload` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, or None when
+    the summary was taken on a different revision of any of the kernels' source files."""
     try:
-        entry = json.load(open(TRAFFIC_SUMMARY))[kernel]
-    except (OSError, ValueError, KeyError):
+        entry = json.load(open(TRAFFIC_SUMMARY))[workload]
+        if entry["sources_sha256_16"] != [source_hash(src) for src in entry["sources"]]:
+            return None
+    except (OSError, ValueError, KeyError, TypeError):
         return None
-    if entry.get("source_sha256_16") != source_hash(entry.get("source", "")):
-        return None
-    return entry.get("hbm_bytes_per_launch")
+    return entry.get("hbm_bytes_per_call")
 
 
 def bench_prefill(gdr, workloads, torch, steps, warmup):
@@ -197,7 +197,9 @@ def bench_verify(gdr, workloads, torch, warmup):
             "verify_gbs": round(gbs(vb, v_ms), 1), "commit_gbs": round(gbs(cb, c_ms), 1),
             "accepted_tokens_per_s": round(mean_accepted / (y_ms * 1e-3), 1),
             "roofline": {"bound": "hbm", "achieved": round(gbs(vb + cb, y_ms), 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(gbs(vb + cb, y_ms) / HBM_PEAK_GBS, 4)}}
+                         "unit": "GB/s", "frac": round(gbs(vb + cb, y_ms) / HBM_PEAK_GBS, 4),
+                         "traffic_verify": committed_traffic("recurrent_kda_verify"),
+                         "traffic_commit": committed_traffic("recurrent_kda_commit")}}
 
 
 def bench_varlen(gdr, workloads, torch, steps, warmup):
@@ -278,7 +280,8 @@ def bench_train(gdr, workloads, torch, steps, warmup):
             "V": cfg["V"], "ms_forward": round(fwd_ms, 4), "ms_backward": round(bwd_ms, 4),
             "tokens_per_s_fwd_bwd": round(tokens / (tot_ms * 1e-3), 1),
             "backward_algorithmic_bytes": nbytes, "backward_gbs": round(nbytes / (bwd_ms * 1e-3) / 1e9, 1),
-            "backward_hbm_frac": round(nbytes / (bwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "backward_hbm_frac": round(nbytes / (bwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "backward_traffic": committed_traffic("chunk_kda_backward")}
 
 
 def cpu_baseline(workloads, torch, budget_s):

@@ -18,10 +18,10 @@
 // and the rank-1 update is applied in place in registers before the single store.  Only the tiny per-token
 // vectors go through LDS.
 //
-// Speculative verify (kRecord) is the same kernel over the 1 + draft tokens of a block, writing each token's update
-// row u_t to an fp32 record as well; recurrent_commit_kernel rebuilds the state after any accepted prefix from the
-// block's initial state, k, the gate and that record, with the same fp32 operations in the same order, so its state
-// after all T tokens equals the verify kernel's final state bit for bit.
+// Speculative verify (recurrent_verify_kernel) runs the same body over the 1 + draft tokens of a block and writes
+// each token's update row u_t to an fp32 record as well; recurrent_commit_kernel rebuilds the state after any
+// accepted prefix from the block's initial state, k, the gate and that record, with the same fp32 operations in the
+// same order, so its state after all T tokens equals the verify kernel's final state bit for bit.
 #include "gdr_common.h"
 #include "gdr_internal.h"
 
@@ -54,10 +54,9 @@ __device__ __forceinline__ float half_swap_sum(float x) {
 
 // q, k and v share one element type InT (bf16 or fp32; the host widens mixed or fp16 inputs to fp32, exactly), so
 // every load has a static type and the compiler can track each one's completion precisely.
-// Occupancy floor of 4 waves per SIMD (at most 128 VGPRs): two 512-thread workgroups per CU, which the group-staging
-// address arithmetic would otherwise push down to one.
+// The body of the decode kernel and of the verify kernel (kRecord: also store each token's update row).
 template <int VARIANT, int K, int VS, int kThreads, typename InT, bool kH0, bool kRecord>
-__global__ __launch_bounds__(kThreads, 4) void recurrent_fwd_kernel(const gdr_args a, int n_slices, float* updates) {
+__device__ __forceinline__ void recurrent_body(const gdr_args& a, int n_slices, float* updates) {
   constexpr int kWaves = kThreads / kWave;
   constexpr int NQ = VS / 4;           // float4 column quads per state row slice
   constexpr int RG = kThreads / NQ;    // row groups
@@ -255,6 +254,20 @@ __global__ __launch_bounds__(kThreads, 4) void recurrent_fwd_kernel(const gdr_ar
   }
 }
 
+// Two kernels (so profiles tell them apart) over one body.  Occupancy floor of 4 waves per SIMD (at most 128
+// VGPRs): two 512-thread workgroups per CU, which the group-staging address arithmetic would otherwise push down to
+// one.
+template <int VARIANT, int K, int VS, int kThreads, typename InT, bool kH0>
+__global__ __launch_bounds__(kThreads, 4) void recurrent_fwd_kernel(const gdr_args a, int n_slices) {
+  recurrent_body<VARIANT, K, VS, kThreads, InT, kH0, false>(a, n_slices, nullptr);
+}
+
+template <int VARIANT, int K, int VS, int kThreads, typename InT, bool kH0>
+__global__ __launch_bounds__(kThreads, 4) void recurrent_verify_kernel(const gdr_args a, int n_slices,
+                                                                       float* updates) {
+  recurrent_body<VARIANT, K, VS, kThreads, InT, kH0, true>(a, n_slices, updates);
+}
+
 // State after the first n_b = clamp(accepted[b], 0, T) tokens of a verified block (all T when `accepted` is NULL):
 //   S = h0;  for t < n_b:  S <- decay_t S;  S <- S + k_t^T u_t      (u_t from the verify kernel's record)
 // Same workgroup tiling as the recurrent kernel (one [K, VS] column slice per workgroup, float4 column quads held in
@@ -345,11 +358,11 @@ static void launch_shape(const gdr_args& a, hipStream_t stream, RecMode mode, co
     hipLaunchKernelGGL((recurrent_commit_kernel<VARIANT, K, VS, kThreads, InT, kH0>), grid, block, 0, stream, a,
                        n_slices, x.updates, x.accepted);
   else if (mode == RecMode::kVerify)
-    hipLaunchKernelGGL((recurrent_fwd_kernel<VARIANT, K, VS, kThreads, InT, kH0, true>), grid, block, 0, stream, a,
+    hipLaunchKernelGGL((recurrent_verify_kernel<VARIANT, K, VS, kThreads, InT, kH0>), grid, block, 0, stream, a,
                        n_slices, x.record);
   else
-    hipLaunchKernelGGL((recurrent_fwd_kernel<VARIANT, K, VS, kThreads, InT, kH0, false>), grid, block, 0, stream, a,
-                       n_slices, nullptr);
+    hipLaunchKernelGGL((recurrent_fwd_kernel<VARIANT, K, VS, kThreads, InT, kH0>), grid, block, 0, stream, a,
+                       n_slices);
 }
 
 template <int VARIANT, int K, typename InT, bool kH0>
