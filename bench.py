@@ -15,6 +15,9 @@ One JSON line on stdout:
   * verify: a speculative-decoding cycle at the decode configuration's state size (batch 256, 16 heads, 128 x 128
     fp32 state) on 8-token blocks: verify (gdr_recurrent_verify, no final state) then commit of a per-sequence
     accepted prefix drawn on the device (gdr_recurrent_commit), in algorithmic GB/s per kernel and per cycle.
+  * fused: the prefill configuration from the KDA layer's pre-op tensors (q, k before normalisation, beta logits,
+    the gate's rank-128 activations with decay_proj[1]'s weight and bias), as one gdr_chunk_fwd_fused call, beside
+    the same preparation done in PyTorch followed by the plain op (what the reference layer runs).
   * train: the prefill configuration under torch.autograd, forward then backward (gdr_chunk_bwd), with the
     backward's algorithmic bytes and HBM fraction.
   * cpu_baseline: the reference's CPU path for the op (fp32 token loop, restated in oracle/) timed on this
@@ -202,6 +205,66 @@ def bench_verify(gdr, workloads, torch, warmup):
                          "traffic_commit": committed_traffic("recurrent_kda_commit")}}
 
 
+def fused_bytes(B, T, H, K, V, R=128, **_):
+    """Algorithmic bytes of one fused-prologue call: q, k, v (bf16) and beta logits per token and head, z (bf16) per
+    token, decay_proj[1]'s weight (bf16) and bias and A_log once, out (bf16), h0 and the final state."""
+    bf16, f32 = 2, 4
+    per_token_head = 2 * K * bf16 + V * bf16 + f32 + V * bf16
+    return B * T * H * per_token_head + B * T * R * bf16 + H * K * (R * bf16 + f32) + H * f32 + 2 * B * H * K * V * f32
+
+
+def bench_fused(gdr, torch, steps, warmup):
+    import math
+    cfg = dict(PREFILL, R=128)
+    B, T, H, K, V, R = cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"], cfg["R"]
+    gen = torch.Generator("cpu").manual_seed(11)
+    dev = "cuda"
+    q = (torch.randn(B, T, H, K, generator=gen) * 3).bfloat16().to(dev).transpose(1, 2)
+    k = (torch.randn(B, T, H, K, generator=gen) * 3).bfloat16().to(dev).transpose(1, 2)
+    v = torch.randn(B, T, H, V, generator=gen).bfloat16().to(dev).transpose(1, 2)
+    z = torch.randn(B, T, R, generator=gen).bfloat16().to(dev)
+    w = (torch.randn(H * K, R, generator=gen) / math.sqrt(R)).bfloat16().to(dev)
+    dt = torch.exp(torch.empty(H * K).uniform_(math.log(1e-3), math.log(1e-1), generator=gen))
+    bias = (dt + torch.log(-torch.expm1(-dt))).to(dev)
+    a_log = torch.log(torch.empty(H).uniform_(1, 16, generator=gen)).to(dev)
+    logits = torch.randn(B, T, H, generator=gen).to(dev).transpose(1, 2)
+    h0 = (torch.randn(B, H, K, V, generator=gen) * 0.02).to(dev)
+    F = torch.nn.functional
+
+    def fused():
+        return gdr.chunk_kimi_delta_attention_fused(q, k, v, z, w, bias, a_log, logits, initial_state=h0,
+                                                    output_final_state=True)
+
+    def unfused():  # the reference layer's preparation (src/layers/kimi_delta_attention.py:45-49), then the op
+        qn = F.normalize(q.float(), dim=-1).bfloat16()
+        kn = F.normalize(k.float(), dim=-1).bfloat16()
+        gate = -a_log.exp()[:, None] * F.softplus(F.linear(z, w, bias.bfloat16()).float().view(B, T, H, K))
+        return gdr.chunk_kimi_delta_attention(qn, kn, v, gate.transpose(1, 2), logits.sigmoid(), initial_state=h0,
+                                              output_final_state=True)
+
+    stream = torch.cuda.current_stream()
+    res = {}
+    with torch.no_grad():
+        for name, fn in (("fused", fused), ("torch_prologue_plus_op", unfused)):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(steps):
+                fn()
+            stop.record(stream)
+            torch.cuda.synchronize()
+            res[name] = start.elapsed_time(stop) / steps
+    nbytes = fused_bytes(**cfg)
+    gbs = nbytes / (res["fused"] * 1e-3) / 1e9
+    return {"workload": "kda_chunk_prefill_fused_prologue", **{x: cfg[x] for x in ("B", "T", "H", "K", "V", "R")},
+            "ms_fused": round(res["fused"], 4), "ms_torch_prologue_plus_op": round(res["torch_prologue_plus_op"], 4),
+            "tokens_per_s": round(B * T / (res["fused"] * 1e-3), 1), "algorithmic_bytes": nbytes,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
 def bench_varlen(gdr, workloads, torch, steps, warmup):
     """The packed-prefill configuration's KDA op: 32 sequences with lengths ~U[256, 4096] (seeded) packed via
     cu_seqlens, H=16, dk=dv=128, per-sequence initial state ~ N(0, 0.02)."""
@@ -313,6 +376,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-verify", action="store_true", help="skip the speculative verify + commit leg")
+    ap.add_argument("--no-fused", action="store_true", help="skip the fused-prologue prefill leg")
     ap.add_argument("--no-varlen", action="store_true", help="skip the packed varlen prefill leg")
     ap.add_argument("--no-train", action="store_true", help="skip the forward + backward (autograd) leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="minimum seconds of CPU baseline work")
@@ -365,6 +429,8 @@ def main():
         record["decode"] = bench_decode(gdr, workloads, torch, warmup=20)
     if not opts.no_verify:
         record["verify"] = bench_verify(gdr, workloads, torch, warmup=10)
+    if not opts.no_fused:
+        record["fused"] = bench_fused(gdr, torch, steps=20, warmup=5)
     if not opts.no_varlen:
         record["varlen"] = bench_varlen(gdr, workloads, torch, steps=10, warmup=3)
     if not opts.no_train:

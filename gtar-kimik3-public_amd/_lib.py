@@ -18,7 +18,8 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.join(_HERE, "libgdr.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
+PRO_NORM_QK, PRO_BETA_LOGITS, PRO_GATE_LOWRANK = 1, 2, 4
 
 KDA, GDN, GLA, DELTANET = 0, 1, 2, 3
 F32, BF16, F16 = 0, 1, 2
@@ -62,6 +63,17 @@ class GdrArgs(ctypes.Structure):
     ]
 
 
+class GdrPrologue(ctypes.Structure):
+    _fields_ = [
+        ("flags", ctypes.c_int32),
+        ("rank", ctypes.c_int32),
+        ("gate_lowrank", GdrTensor),
+        ("gate_weight", ctypes.c_void_p),
+        ("gate_bias", ctypes.c_void_p),
+        ("a_log", ctypes.c_void_p),
+    ]
+
+
 class GdrGrads(ctypes.Structure):
     _fields_ = [
         ("d_out", GdrTensor),
@@ -81,6 +93,7 @@ EXPORTS = {
                                      ctypes.c_int64, ctypes.c_void_p]),
     "gdr_chunk_bwd_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(GdrArgs)]),
     "gdr_chunk_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
+    "gdr_chunk_fwd_fused": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.POINTER(GdrPrologue), ctypes.c_void_p]),
     "gdr_chunk_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(GdrArgs)]),
     "gdr_recurrent_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
     "gdr_recurrent_verify": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p]),
@@ -220,3 +233,26 @@ def commit(args: GdrArgs, updates: torch.Tensor, accepted: torch.Tensor | None, 
     acc = ctypes.c_void_p(accepted.data_ptr()) if accepted is not None else None
     _check("gdr_recurrent_commit", lib.gdr_recurrent_commit(ctypes.byref(args), ctypes.c_void_p(updates.data_ptr()),
                                                             acc, ctypes.c_void_p(stream)))
+
+
+def make_prologue(flags: int, gate_lowrank=None, gate_weight=None, gate_bias=None, a_log=None) -> GdrPrologue:
+    pro = GdrPrologue()
+    pro.flags = flags
+    if gate_lowrank is not None:
+        pro.rank = gate_lowrank.shape[-1]
+        view = GdrTensor()
+        view.ptr, view.dtype = gate_lowrank.data_ptr(), _DTYPE_CODES[gate_lowrank.dtype]
+        view.stride_b, view.stride_h, view.stride_t = gate_lowrank.stride(0), 0, gate_lowrank.stride(1)
+        pro.gate_lowrank = view
+        pro.gate_weight = gate_weight.data_ptr()
+        pro.gate_bias = gate_bias.data_ptr() if gate_bias is not None else None
+        pro.a_log = a_log.data_ptr()
+    return pro
+
+
+def launch_fused(args: GdrArgs, pro: GdrPrologue, device: torch.device) -> None:
+    """Enqueue gdr_chunk_fwd_fused on torch's current stream (args carries the workspace)."""
+    lib = load_library()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    _check("gdr_chunk_fwd_fused", lib.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro),
+                                                          ctypes.c_void_p(stream)))

@@ -338,11 +338,8 @@ __device__ __forceinline__ void producer_loop(const ChunkCtx& x, unsigned char* 
       if constexpr (kGate) {
         if (__any(hot_mask != 0)) {
           __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-          hot_diag_fixup<K, kDelta, kGate, 0>(x, s * kChunk, PW, hot_mask, buf + M::Sc + tri_tile(PW, PW) * 256,
-                                              lii, bbeta + kRow0);
-          __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-          hot_diag_fixup<K, kDelta, kGate, 4>(x, s * kChunk, PW, hot_mask, buf + M::Sc + tri_tile(PW, PW) * 256,
-                                              lii, bbeta + kRow0);
+          hot_diag_fixup<K, kDelta>(s * kChunk, PW, x.len, hot_mask, buf + M::Sc + tri_tile(PW, PW) * 256, lii,
+                                    bbeta + kRow0, InputRows{x, kGate});
         }
       }
       // ---- chunk s + 1 becomes current ----

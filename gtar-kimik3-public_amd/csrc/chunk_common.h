@@ -53,6 +53,7 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 
 // Per-workgroup view of the problem: base pointers already offset to (sequence, head), strides, lengths.
 struct ChunkCtx {
@@ -70,94 +71,75 @@ struct ChunkCtx {
   float scale;
 };
 
-// Exact evaluation of the diagonal 16x16 block of the gated scores and kernel matrix for the channels of this
-// lane whose in-block decay span is too large for the block-start factorisation (bit c of hot_mask <-> channel
-// c0 + c).  Re-reads the block's q, k and gate rows (L2-resident), rebuilds the in-block cumulative gate and adds
-//   Sc(t, s) += sum_{hot c} q_tc k_sc e^{b_tc - b_sc}   (t >= s),   L(t, s) += beta_t sum_{hot c} k_tc k_sc e^{...}  (t > s)
-// to the tiles the MFMA pass produced with zero key operands for those channels.
-template <int K, bool kDelta, int kGate, int CH0>
-__device__ __forceinline__ void hot_diag_fixup(const ChunkCtx& x, int chunk_row0, int pw, uint32_t hot_mask,
-                                               __bf16* sc_tile, float* lii_tile, const float* beta_rows) {
-  // one pass over the 4 channels c0 + CH0 .. c0 + CH0 + 3 of this lane (two passes keep the live data small)
-  constexpr int LPR = K / 8, RSG = kWave / LPR, RPL = 16 / RSG, NC = 4;
+// Inclusive prefix sum over the 16 lanes of each DPP row (v_add_f32 with row_shr:1, 2, 4, 8; lanes shifted in from
+// outside the row contribute 0).
+__device__ __forceinline__ float row_scan16(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, true));
+  return x;
+}
+
+// One channel of one row of the op's inputs, for the hot-channel fix-up: q, k (bf16) and the gate (per channel for
+// KDA / GLA, per token for GDN).
+struct InputRows {
+  const ChunkCtx& x;
+  int gate_mode;  // 2: per-channel gate, 1: scalar gate
+  __device__ __forceinline__ void operator()(int tc, int ch, float& q, float& k, float& g) const {
+    q = static_cast<float>(x.qp[tc * x.q_st + ch]);
+    k = static_cast<float>(x.kp[tc * x.k_st + ch]);
+    g = gate_mode == 2 ? x.gp[tc * x.g_st + ch] : x.gp[tc * x.g_st];
+  }
+};
+
+// Exact evaluation of the diagonal 16x16 block of the gated scores and kernel matrix for the channels whose
+// in-block decay span is too large for the block-start factorisation (hot channels; the MFMA pass gave them zero key
+// operands).  Hot channels are rare and usually few per block, so they are taken one at a time: lanes 0..15 hold
+// the 16 rows' q, k and gate of the channel and form its in-block cumulative log2 gate b with a DPP row scan, and
+// lane L adds the channel's share to the four entries (t, s) = (L / 4, 4 (L % 4) + i):
+//   Sc(t, s) += q_t k_s e^{b_t - b_s}  (t >= s),    L(t, s) += beta_t k_t k_s e^{b_t - b_s}  (t > s).
+// hot_mask: on lanes with lane % (K / 8) == grp, bit m marks channel 8 grp + m.  `fetch(tc, ch, q, k, g)` is called
+// by all 64 lanes (wave-uniform channel ch, tc the clamped token of row lane % 16) and returns that row's q, k and
+// gate (natural-log units) for channel ch.
+template <int K, bool kDelta, typename Fetch>
+__device__ __forceinline__ void hot_diag_fixup(int chunk_row0, int pw, int len, uint32_t hot_mask, __bf16* sc_tile,
+                                               float* lii_tile, const float* beta_rows, const Fetch& fetch) {
+  constexpr int LPR = K / 8;
   const int lane = threadIdx.x & 63;
-  const int cg = lane % LPR, rs = lane / LPR, c0 = 8 * cg + CH0;
-  float hq[RPL][NC], hk[RPL][NC], hb[RPL][NC];
+  const int t_seq = chunk_row0 + 16 * pw + (lane & 15);
+  const int tc = min(t_seq, len - 1);
+  const bool ok = t_seq < len;
+  const int tt = lane >> 2, s0 = 4 * (lane & 3);
+  float sc_acc[4] = {0.f, 0.f, 0.f, 0.f}, p_acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int grp = 0; grp < LPR; ++grp) {
+    uint32_t m = __shfl(hot_mask, grp, kWave);  // wave-uniform
+    while (m) {
+      const int ch = 8 * grp + __builtin_ctz(m);
+      m &= m - 1;
+      float q, k, g;
+      fetch(tc, ch, q, k, g);
+      if (!ok) q = k = g = 0.f;
+      const float b = row_scan16(g * kLog2e);
+      const float qt = __shfl(q, tt, kWave), kt = __shfl(k, tt, kWave), bt = __shfl(b, tt, kWave);
 #pragma unroll
-  for (int j = 0; j < RPL; ++j) {
-    const int t = chunk_row0 + 16 * pw + rs * RPL + j;
-    const int tc = min(t, x.len - 1);
-    const bool ok = t < x.len;
-    const uint2 qv = *reinterpret_cast<const uint2*>(x.qp + tc * x.q_st + c0);
-    const uint2 kv = *reinterpret_cast<const uint2*>(x.kp + tc * x.k_st + c0);
-    const uint32_t qw[2] = {qv.x, qv.y}, kw[2] = {kv.x, kv.y};
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const float qe = __uint_as_float((c & 1) ? (qw[c >> 1] & 0xffff0000u) : (qw[c >> 1] << 16));
-      const float ke = __uint_as_float((c & 1) ? (kw[c >> 1] & 0xffff0000u) : (kw[c >> 1] << 16));
-      const float g = kGate == 2 ? x.gp[tc * x.g_st + c0 + c] : x.gp[tc * x.g_st];
-      hq[j][c] = ok ? qe : 0.f;
-      hk[j][c] = ok ? ke : 0.f;
-      hb[j][c] = ok ? g * kLog2e : 0.f;
+      for (int i = 0; i < 4; ++i) {
+        const int sr = s0 + i;
+        const float ks = __shfl(k, sr, kWave), bs = __shfl(b, sr, kWave);
+        const float d = ks * __builtin_amdgcn_exp2f(fminf(bt - bs, 0.f));
+        if (tt >= sr) sc_acc[i] += qt * d;
+        if (kDelta && tt > sr) p_acc[i] += kt * d;
+      }
     }
   }
 #pragma unroll
-  for (int j = 1; j < RPL; ++j)
-#pragma unroll
-    for (int c = 0; c < NC; ++c) hb[j][c] += hb[j - 1][c];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const float own = hb[RPL - 1][c];
-    float incl = own;
-#pragma unroll
-    for (int off = LPR; off < kWave; off *= 2) {
-      const float y = __shfl_up(incl, off, kWave);
-      if (lane >= off) incl += y;
+  for (int i = 0; i < 4; ++i) {
+    const int sr = s0 + i;
+    if (tt >= sr) {
+      __bf16* dst = sc_tile + tt * 16 + sr;
+      *dst = bf(f32(*dst) + sc_acc[i]);
     }
-#pragma unroll
-    for (int j = 0; j < RPL; ++j) hb[j][c] += incl - own;
-  }
-#pragma unroll 1
-  for (int sr = 0; sr < 16; ++sr) {
-    const int src = cg + LPR * (sr / RPL);
-    const int js = sr % RPL;
-    float pa[RPL], sa[RPL];
-#pragma unroll
-    for (int j = 0; j < RPL; ++j) pa[j] = sa[j] = 0.f;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      float kv = 0.f, bv = 0.f;
-#pragma unroll
-      for (int jj = 0; jj < RPL; ++jj) {
-        if (jj == js) {
-          kv = hk[jj][c];
-          bv = hb[jj][c];
-        }
-      }
-      const float ks = __shfl(kv, src, kWave), bs = __shfl(bv, src, kWave);
-      if (hot_mask & (1u << (CH0 + c))) {
-#pragma unroll
-        for (int j = 0; j < RPL; ++j) {
-          const float d = ks * __builtin_amdgcn_exp2f(fminf(hb[j][c] - bs, 0.f));
-          pa[j] += hk[j][c] * d;
-          sa[j] += hq[j][c] * d;
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < RPL; ++j) {
-#pragma unroll
-      for (int m = 1; m < LPR; m *= 2) {
-        pa[j] += shfl_xor(pa[j], m);
-        sa[j] += shfl_xor(sa[j], m);
-      }
-      const int t = rs * RPL + j;
-      if (cg == 0 && t >= sr) {
-        __bf16* dst = sc_tile + t * 16 + sr;
-        *dst = bf(f32(*dst) + sa[j]);
-        if (kDelta && t > sr) lii_tile[t * 16 + sr] += beta_rows[t] * pa[j];
-      }
-    }
+    if (kDelta && tt > sr) lii_tile[tt * 16 + sr] += beta_rows[tt] * p_acc[i];
   }
 }
 

@@ -55,14 +55,76 @@ struct PrepLds {
   static constexpr int RDS = TOT + 4 * K * 4;     // fp32 [4][K]    diagonal key factor e^{-T_i} (0: hot channel)
   static constexpr int FAR = RDS + 4 * K * 4;     // fp32 [3][K]    key factors of tiles (2,0), (3,0), (3,1)
   static constexpr int BETA = FAR + 3 * K * 4;    // fp32 [64]
-  static constexpr int BYTES = BETA + 256;
+  static constexpr int NRM = BETA + 256;          // fp32 [2][64]   fused prologue: 1 / ||q||, 1 / ||k|| per row
+  static constexpr int BYTES = NRM + 512;
   static_assert(8 * K * 4 <= 16 * 512, "EPRE/ETAIL alias");
   static_assert(4 * 512 <= 11 * K * 4, "AINV alias");
 };
 
+// softplus(x) = max(x, 0) + log1p(e^{-|x|}) in fp32.  log1p(y) for y in (0, 1] as log(u) * y / (u - 1) with u = 1 + y
+// (exact to a few ulp even where u rounds to 1 + y's leading bits: the rounding error of u cancels in the ratio).
+__device__ __forceinline__ float softplus_f32(float x) {
+  const float y = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e);
+  const float u = 1.f + y;
+  const float l1p = u == 1.f ? y : __builtin_amdgcn_logf(u) * kLn2 * __fdividef(y, u - 1.f);
+  return fmaxf(x, 0.f) + l1p;
+}
+
+// The low-rank gate of the fused prologue for the chunk's 64 rows:
+//   g[t][c] = -e^{A_log[h]} softplus(z_t . W[h K + c] + bias[h K + c])
+// Wave w computes channels [w K / 4, (w + 1) K / 4) of all 64 rows as Gᵀ = W_h Zᵀ on v_mfma_f32_16x16x32_bf16 (A = 16
+// channels x 32 of R from W's rows, B = 32 of R x 16 tokens from z's rows), so each wave reads only its quarter of W
+// (the rows of z are shared through L2).  Lane (l16, g4) ends with channels 16 t + 4 g4 + i of token 16 j + l16; the
+// values go to the fp32 LDS rows `gst` (row pitch K + 4), from which every lane later reads its own row.
+template <int K>
+__device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h, const __bf16* zchunk, int64_t z_st,
+                                                  int last_row, float* gst, int wave, int l16, int g4) {
+  constexpr int CT = K / 64;  // 16-channel tiles per wave
+  const int R = pro.rank, ch0 = wave * (K / 4);
+  const __bf16* w = static_cast<const __bf16*>(pro.gate_weight) + (size_t(h) * K + ch0 + l16) * R + 8 * g4;
+  const __bf16* zr[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) zr[j] = zchunk + int64_t(min(16 * j + l16, last_row)) * z_st + 8 * g4;
+  floatx4 acc[CT][4];
+#pragma unroll
+  for (int t = 0; t < CT; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[t][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < R / 32; ++s) {  // the accumulators start at zero right before this loop
+    bf16x8 zb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) zb[j] = *reinterpret_cast<const bf16x8*>(zr[j] + 32 * s);
+#pragma unroll
+    for (int t = 0; t < CT; ++t) {
+      const bf16x8 wa = *reinterpret_cast<const bf16x8*>(w + size_t(16 * t) * R + 32 * s);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[t][j] = mfma32(wa, zb[j], acc[t][j]);
+    }
+  }
+  const float neg_a = -__builtin_amdgcn_exp2f(pro.a_log[h] * kLog2e);
+#pragma unroll
+  for (int t = 0; t < CT; ++t) {
+    const int ch = ch0 + 16 * t + 4 * g4;
+    float4 bias = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (pro.gate_bias) bias = *reinterpret_cast<const float4*>(pro.gate_bias + size_t(h) * K + ch);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 g = make_float4(
+          neg_a * softplus_f32(acc[t][j][0] + bias.x), neg_a * softplus_f32(acc[t][j][1] + bias.y),
+          neg_a * softplus_f32(acc[t][j][2] + bias.z), neg_a * softplus_f32(acc[t][j][3] + bias.w));
+      *reinterpret_cast<float4*>(gst + (16 * j + l16) * (K + 4) + ch) = g;
+    }
+  }
+}
+
 // ======================================= prep: one workgroup per (chunk, head) =======================================
-template <int VARIANT, int K>
-__global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int nc, int64_t rec_bytes) {
+// kPro: the fused layer prologue.  0: none (the plain op); 1: `pro.flags` selects the in-kernel q / k
+// normalisation and the beta sigmoid; 2: as 1, and the per-channel gate comes from the low-rank projection.
+template <int VARIANT, int K, int kPro = 0>
+__global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr_args a, int nc, int64_t rec_bytes,
+                                                                       const gdr_prologue pro) {
+  constexpr bool kLowRank = kPro == 2;
+  static_assert(!kLowRank || VARIANT == GDR_KDA || VARIANT == GDR_GLA, "low-rank gate: per-channel variants");
   constexpr bool kDelta = VARIANT != GDR_GLA;
   constexpr int kGate = (VARIANT == GDR_KDA || VARIANT == GDR_GLA) ? 2 : (VARIANT == GDR_GDN ? 1 : 0);
   constexpr int KS = K / 32;
@@ -121,6 +183,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
   float* rds = reinterpret_cast<float*>(smem + L::RDS);
   float* far = reinterpret_cast<float*>(smem + L::FAR);
   float* sbeta = reinterpret_cast<float*>(smem + L::BETA);
+  float* snorm = reinterpret_cast<float*>(smem + L::NRM);
 
   // A-operand lane layout: lane (l16, g4) of wave p holds row 16 p + l16, channels 32 kk + 8 g4 + j.
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, g4 = lane >> 4;
@@ -162,12 +225,26 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
   // ---- 1. loads: this lane's q, k, gate, beta row; the first pass of V ----
   uint4 qraw[KS], kraw[KS];
   float bl[KS][8];
+  if constexpr (kLowRank) {
+    // The gate rows are computed into the KAP / KD region, which nothing uses before step 3b (after two barriers).
+    const __bf16* zchunk = static_cast<const __bf16*>(pro.gate_lowrank.ptr) + bidx * pro.gate_lowrank.stride_b +
+                           int64_t(bos + c * kChunk) * pro.gate_lowrank.stride_t;
+    lowrank_gate_rows<K>(pro, h, zchunk, pro.gate_lowrank.stride_t, len - 1 - c * kChunk,
+                         reinterpret_cast<float*>(smem), wave, l16, g4);
+    __syncthreads();
+  }
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {
     const int ch = 32 * kk + 8 * g4;
     qraw[kk] = *reinterpret_cast<const uint4*>(x.qp + tc * x.q_st + ch);
     kraw[kk] = *reinterpret_cast<const uint4*>(x.kp + tc * x.k_st + ch);
-    if constexpr (kGate == 2) {
+    if constexpr (kLowRank) {
+      const float* gr = reinterpret_cast<const float*>(smem) + (16 * p + l16) * (K + 4) + ch;
+      const float4 g0 = *reinterpret_cast<const float4*>(gr);
+      const float4 g1 = *reinterpret_cast<const float4*>(gr + 4);
+      bl[kk][0] = g0.x; bl[kk][1] = g0.y; bl[kk][2] = g0.z; bl[kk][3] = g0.w;
+      bl[kk][4] = g1.x; bl[kk][5] = g1.y; bl[kk][6] = g1.z; bl[kk][7] = g1.w;
+    } else if constexpr (kGate == 2) {
       const float4 g0 = *reinterpret_cast<const float4*>(x.gp + tc * x.g_st + ch);
       const float4 g1 = *reinterpret_cast<const float4*>(x.gp + tc * x.g_st + ch + 4);
       bl[kk][0] = g0.x; bl[kk][1] = g0.y; bl[kk][2] = g0.z; bl[kk][3] = g0.w;
@@ -187,7 +264,37 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
 #pragma unroll
       for (int j = 0; j < 8; ++j) bl[kk][j] = 0.f;
   }
-  const float beta_t = kDelta ? x.betap[tc * x.b_st] : 0.f;
+  float beta_t = kDelta ? x.betap[tc * x.b_st] : 0.f;
+  if (kPro && kDelta && (pro.flags & GDR_PRO_BETA_LOGITS))
+    beta_t = 1.f / (1.f + __builtin_amdgcn_exp2f(-beta_t * kLog2e));
+  if (kPro && (pro.flags & GDR_PRO_NORM_QK)) {  // F.normalize over the K channels of this row (spread over the 4 lanes g4)
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      float qf[8], kf[8];
+      unpack8(qraw[kk], qf);
+      unpack8(kraw[kk], kf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sq += qf[j] * qf[j], sk += kf[j] * kf[j];
+    }
+    sq += __shfl_xor(sq, 16, kWave);
+    sk += __shfl_xor(sk, 16, kWave);
+    sq += __shfl_xor(sq, 32, kWave);
+    sk += __shfl_xor(sk, 32, kWave);
+    const float iq = 1.f / fmaxf(sqrtf(sq), 1e-12f), ik = 1.f / fmaxf(sqrtf(sk), 1e-12f);
+    if (g4 == 0) snorm[16 * p + l16] = iq, snorm[64 + 16 * p + l16] = ik;  // for the hot-block fix-up
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      float qf[8], kf[8];
+      unpack8(qraw[kk], qf);
+      unpack8(kraw[kk], kf);
+      bf16x8 nq, nk;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) nq[j] = bf(qf[j] * iq), nk[j] = bf(kf[j] * ik);
+      qraw[kk] = *reinterpret_cast<const uint4*>(&nq);
+      kraw[kk] = *reinterpret_cast<const uint4*>(&nk);
+    }
+  }
   load_v_pass(0);
 
   // ---- 2. in-block inclusive cumsum of the log2 gate over the 16 rows (one DPP row per channel group) ----
@@ -335,11 +442,42 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const gdr_args a, int n
     for (int m = 0; m < 8; ++m) hot_mask |= (-tot[p * K + 8 * cgh + m] > kHot) ? (1u << m) : 0u;
     if (__any(hot_mask != 0)) {
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      hot_diag_fixup<K, kDelta, kGate, 0>(x, c * kChunk, p, hot_mask, sct + tri_tile(p, p) * 256, lii + p * 256,
-                                          sbeta + 16 * p);
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      hot_diag_fixup<K, kDelta, kGate, 4>(x, c * kChunk, p, hot_mask, sct + tri_tile(p, p) * 256, lii + p * 256,
-                                          sbeta + 16 * p);
+      auto fixup = [&](const auto& rows) {
+        hot_diag_fixup<K, kDelta>(c * kChunk, p, len, hot_mask, sct + tri_tile(p, p) * 256, lii + p * 256,
+                                  sbeta + 16 * p, rows);
+      };
+      if (kPro && (kLowRank || (pro.flags & GDR_PRO_NORM_QK))) {
+        // The fused prologue's inputs are not in memory as the kernel used them: q, k are renormalised with the
+        // row norms kept in LDS, and the gate is recomputed from z and W (the R-long dot split over the 4 lanes
+        // that share a row).
+        const bool norm = pro.flags & GDR_PRO_NORM_QK;
+        auto rows = [&](int tcr, int ch, float& q, float& k, float& g) {
+          InputRows{x, kGate}(tcr, ch, q, k, g);  // g is replaced below when it is computed
+          const int r = tcr - c * kChunk;          // row within the chunk (clamped rows stay inside it)
+          if (norm) q = f32(bf(q * snorm[r])), k = f32(bf(k * snorm[64 + r]));
+          if constexpr (kLowRank) {
+            const int R = pro.rank, part = lane >> 4, span = R / 4;
+            const __bf16* zr = static_cast<const __bf16*>(pro.gate_lowrank.ptr) + bidx * pro.gate_lowrank.stride_b +
+                               int64_t(bos + tcr) * pro.gate_lowrank.stride_t + part * span;
+            const __bf16* wr = static_cast<const __bf16*>(pro.gate_weight) + (size_t(h) * K + ch) * R + part * span;
+            float acc = 0.f;
+            for (int e = 0; e < span; e += 8) {
+              float zf[8], wf[8];
+              unpack8(*reinterpret_cast<const uint4*>(zr + e), zf);
+              unpack8(*reinterpret_cast<const uint4*>(wr + e), wf);
+#pragma unroll
+              for (int j = 0; j < 8; ++j) acc += zf[j] * wf[j];
+            }
+            acc += __shfl_xor(acc, 16, kWave);
+            acc += __shfl_xor(acc, 32, kWave);
+            const float bias = pro.gate_bias ? pro.gate_bias[size_t(h) * K + ch] : 0.f;
+            g = -__builtin_amdgcn_exp2f(pro.a_log[h] * kLog2e) * softplus_f32(acc + bias);
+          }
+        };
+        fixup(rows);
+      } else {
+        fixup(InputRows{x, kGate});
+      }
     }
   }
   lds_barrier();
@@ -673,26 +811,46 @@ int64_t slots_per_head(const gdr_args& a) {
   return int64_t(a.batch) * ((a.seq_len + kChunk - 1) / kChunk);
 }
 
-template <int VARIANT, int K, typename OutT>
-hipError_t launch_split_typed(const gdr_args& a, hipStream_t stream) {
+// Sets a kernel's dynamic-LDS limit once per instantiation (a benign race: every thread sets the same value).
+template <auto Kernel>
+hipError_t configure_lds(int bytes) {
+  static bool done = false;
+  if (done) return hipSuccess;
+  const hipError_t e =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done = true;
+  return e;
+}
+
+template <int VARIANT, int K, int kPro>
+hipError_t launch_prep(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
   const int nc = (a.seq_len + kChunk - 1) / kChunk;
-  const int64_t rec = Rec<K>::bytes(a.value_dim);
   const int64_t n_prep = slots_per_head(a) * a.heads;
   constexpr int prep_lds = PrepLds<K>::BYTES;
-  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::UT_SLICE);
-  static bool configured = false;  // benign race: every thread sets the same attributes
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_prep_kernel<VARIANT, K>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, prep_lds);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_scan_kernel<VARIANT, K, OutT>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, scan_lds);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  hipError_t e = configure_lds<&chunk_prep_kernel<VARIANT, K, kPro>>(prep_lds);
+  if (e != hipSuccess) return e;
   if (n_prep > 0)
-    hipLaunchKernelGGL((chunk_prep_kernel<VARIANT, K>), dim3(unsigned(n_prep)), dim3(256), prep_lds, stream, a, nc,
-                       rec);
+    hipLaunchKernelGGL((chunk_prep_kernel<VARIANT, K, kPro>), dim3(unsigned(n_prep)), dim3(256), prep_lds, stream,
+                       a, nc, Rec<K>::bytes(a.value_dim), pro);
+  return hipGetLastError();
+}
+
+template <int VARIANT, int K, typename OutT>
+hipError_t launch_split_typed(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
+  const int nc = (a.seq_len + kChunk - 1) / kChunk;
+  const int64_t rec = Rec<K>::bytes(a.value_dim);
+  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::UT_SLICE);
+  hipError_t e;
+  if (!pro.flags) {
+    e = launch_prep<VARIANT, K, 0>(a, pro, stream);
+  } else if constexpr (VARIANT == GDR_KDA || VARIANT == GDR_GLA) {
+    e = (pro.flags & GDR_PRO_GATE_LOWRANK) ? launch_prep<VARIANT, K, 2>(a, pro, stream)
+                                           : launch_prep<VARIANT, K, 1>(a, pro, stream);
+  } else {
+    e = launch_prep<VARIANT, K, 1>(a, pro, stream);
+  }
+  if (e == hipSuccess) e = configure_lds<&chunk_scan_kernel<VARIANT, K, OutT>>(scan_lds);
+  if (e != hipSuccess) return e;
   const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
   const int bh = n_seq * a.heads;
   const int n_slices = a.value_dim / kScanSlice;
@@ -703,17 +861,17 @@ hipError_t launch_split_typed(const gdr_args& a, hipStream_t stream) {
 }
 
 template <int VARIANT, int K>
-hipError_t launch_split_k(const gdr_args& a, hipStream_t stream) {
+hipError_t launch_split_k(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
   switch (a.out.dtype) {
-    case GDR_BF16: return launch_split_typed<VARIANT, K, __bf16>(a, stream);
-    case GDR_F16: return launch_split_typed<VARIANT, K, _Float16>(a, stream);
-    default: return launch_split_typed<VARIANT, K, float>(a, stream);
+    case GDR_BF16: return launch_split_typed<VARIANT, K, __bf16>(a, pro, stream);
+    case GDR_F16: return launch_split_typed<VARIANT, K, _Float16>(a, pro, stream);
+    default: return launch_split_typed<VARIANT, K, float>(a, pro, stream);
   }
 }
 
 template <int VARIANT>
-hipError_t launch_split_v(const gdr_args& a, hipStream_t stream) {
-  return a.key_dim == 64 ? launch_split_k<VARIANT, 64>(a, stream) : launch_split_k<VARIANT, 128>(a, stream);
+hipError_t launch_split_v(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
+  return a.key_dim == 64 ? launch_split_k<VARIANT, 64>(a, pro, stream) : launch_split_k<VARIANT, 128>(a, pro, stream);
 }
 
 // Backward recompute: records into the backward workspace, then the scan in its states mode.
@@ -724,22 +882,10 @@ hipError_t launch_states_typed(const gdr_args& fwd, const BwdLayout& L, unsigned
   a.ht = nullptr;
   const int nc = (a.seq_len + kChunk - 1) / kChunk;
   const int64_t rec = Rec<K>::bytes(a.value_dim);
-  const int64_t n_prep = slots_per_head(a) * a.heads;
-  constexpr int prep_lds = PrepLds<K>::BYTES;
   constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::UT_SLICE);
-  static bool configured = false;  // benign race: every thread sets the same attributes
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_prep_kernel<VARIANT, K>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, prep_lds);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_scan_kernel<VARIANT, K, __bf16, true>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, scan_lds);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
-  if (n_prep > 0)
-    hipLaunchKernelGGL((chunk_prep_kernel<VARIANT, K>), dim3(unsigned(n_prep)), dim3(256), prep_lds, stream, a, nc,
-                       rec);
+  hipError_t e = launch_prep<VARIANT, K, 0>(a, gdr_prologue{}, stream);
+  if (e == hipSuccess) e = configure_lds<&chunk_scan_kernel<VARIANT, K, __bf16, true>>(scan_lds);
+  if (e != hipSuccess) return e;
   const int bh = a.batch * a.heads;
   const int n_slices = a.value_dim / kScanSlice;
   const int xcd_map = (bh % 8 == 0) ? 1 : 0;
@@ -771,12 +917,12 @@ hipError_t launch_chunk_states(const gdr_args& a, const BwdLayout& L, unsigned c
   }
 }
 
-hipError_t launch_chunk_split(const gdr_args& a, hipStream_t stream) {
+hipError_t launch_chunk_split(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
   switch (a.variant) {
-    case GDR_KDA: return launch_split_v<GDR_KDA>(a, stream);
-    case GDR_GDN: return launch_split_v<GDR_GDN>(a, stream);
-    case GDR_GLA: return launch_split_v<GDR_GLA>(a, stream);
-    default: return launch_split_v<GDR_DELTANET>(a, stream);
+    case GDR_KDA: return launch_split_v<GDR_KDA>(a, pro, stream);
+    case GDR_GDN: return launch_split_v<GDR_GDN>(a, pro, stream);
+    case GDR_GLA: return launch_split_v<GDR_GLA>(a, pro, stream);
+    default: return launch_split_v<GDR_DELTANET>(a, pro, stream);
   }
 }
 

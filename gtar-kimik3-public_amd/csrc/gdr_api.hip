@@ -57,10 +57,11 @@ int check_shape(const gdr_args* a, bool chunk) {
   return GDR_OK;
 }
 
-int check_common(const gdr_args* a, bool chunk, bool need_out = true) {
+// gate_in_memory false: the fused prologue computes the gate, so args->gate must be NULL.
+int check_common(const gdr_args* a, bool chunk, bool need_out = true, bool gate_in_memory = true) {
   int rc = check_shape(a, chunk);
   if (rc) return rc;
-  const bool has_gate = a->variant != GDR_DELTANET;
+  const bool has_gate = a->variant != GDR_DELTANET && gate_in_memory;
   const bool has_beta = a->variant != GDR_GLA;
   if ((rc = check_view(a->q, "query", true, false))) return rc;
   if ((rc = check_view(a->k, "key", true, false))) return rc;
@@ -68,7 +69,8 @@ int check_common(const gdr_args* a, bool chunk, bool need_out = true) {
   if ((rc = check_view(a->out, "out", need_out, false))) return rc;
   if ((rc = check_view(a->gate, "gate", has_gate, true))) return rc;
   if ((rc = check_view(a->beta, "beta", has_beta, true))) return rc;
-  if (!has_gate && a->gate.ptr) return fail(GDR_ERR_INVALID, "DeltaNet takes no gate");
+  if (!has_gate && a->gate.ptr)
+    return fail(GDR_ERR_INVALID, gate_in_memory ? "DeltaNet takes no gate" : "gate must be NULL: it is computed");
   if (!has_beta && a->beta.ptr) return fail(GDR_ERR_INVALID, "GLA takes no beta");
   if ((reinterpret_cast<uintptr_t>(a->h0) | reinterpret_cast<uintptr_t>(a->ht)) % 16 != 0)
     return fail(GDR_ERR_INVALID, "initial/final state must be 16-byte aligned");
@@ -80,6 +82,70 @@ int check_rows16(const gdr_tensor& t, const char* name) {
   if (reinterpret_cast<uintptr_t>(t.ptr) % 16 || (t.stride_b * es) % 16 || (t.stride_h * es) % 16 ||
       (t.stride_t * es) % 16)
     return fail(GDR_ERR_INVALID, "%s: base pointer and b/h/t strides must be 16-byte aligned", name);
+  return GDR_OK;
+}
+
+// The prologue of gdr_chunk_fwd_fused (no pointer dereferenced).
+int check_prologue(const gdr_args* a, const gdr_prologue* pro) {
+  if (pro->flags & ~(GDR_PRO_NORM_QK | GDR_PRO_BETA_LOGITS | GDR_PRO_GATE_LOWRANK))
+    return fail(GDR_ERR_INVALID, "unknown prologue flags 0x%x", pro->flags);
+  if ((pro->flags & GDR_PRO_BETA_LOGITS) && a->variant == GDR_GLA)
+    return fail(GDR_ERR_INVALID, "GLA takes no beta (GDR_PRO_BETA_LOGITS)");
+  if (!(pro->flags & GDR_PRO_GATE_LOWRANK)) return GDR_OK;
+  if (a->variant != GDR_KDA && a->variant != GDR_GLA)
+    return fail(GDR_ERR_UNSUPPORTED, "the low-rank gate is for the per-channel gates (KDA, GLA)");
+  if (pro->rank < 32 || pro->rank > 512 || pro->rank % 32)
+    return fail(GDR_ERR_UNSUPPORTED, "gate rank %d not supported (a multiple of 32 up to 512)", pro->rank);
+  int rc = check_view(pro->gate_lowrank, "gate_lowrank", true, false);
+  if (rc) return rc;
+  if (pro->gate_lowrank.dtype != GDR_BF16) return fail(GDR_ERR_UNSUPPORTED, "gate_lowrank must be bf16");
+  if (reinterpret_cast<uintptr_t>(pro->gate_lowrank.ptr) % 16 || (pro->gate_lowrank.stride_b * 2) % 16 ||
+      (pro->gate_lowrank.stride_t * 2) % 16)
+    return fail(GDR_ERR_INVALID, "gate_lowrank: base pointer and b/t strides must be 16-byte aligned");
+  if (!pro->gate_weight || reinterpret_cast<uintptr_t>(pro->gate_weight) % 16)
+    return fail(GDR_ERR_INVALID, "gate_weight: null or not 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(pro->gate_bias) % 16)
+    return fail(GDR_ERR_INVALID, "gate_bias must be 16-byte aligned");
+  if (!pro->a_log) return fail(GDR_ERR_INVALID, "a_log: null pointer");
+  return GDR_OK;
+}
+
+int chunk_fwd(const gdr_args* a, const gdr_prologue* pro, hipStream_t stream) {
+  int rc = check_shape(a, true);
+  if (rc) return rc;
+  if (pro && (rc = check_prologue(a, pro))) return rc;
+  const bool lowrank = pro && (pro->flags & GDR_PRO_GATE_LOWRANK);
+  if ((rc = check_common(a, true, true, !lowrank))) return rc;
+  if (pro && !a->workspace) return fail(GDR_ERR_INVALID, "the fused prologue needs a workspace (two-launch path)");
+  if (a->q.dtype != GDR_BF16 || a->k.dtype != GDR_BF16 || a->v.dtype != GDR_BF16)
+    return fail(GDR_ERR_UNSUPPORTED, "chunk mode reads bf16 q, k, v (got dtype codes %d, %d, %d)", a->q.dtype,
+                a->k.dtype, a->v.dtype);
+  // Rows of q, k, v, gate and out are moved with 16-byte accesses.
+  const gdr_tensor* rows[] = {&a->q, &a->k, &a->v, &a->out, &a->gate};
+  const char* names[] = {"query", "key", "value", "out", "gate"};
+  for (int i = 0; i < 5; ++i) {
+    const gdr_tensor& t = *rows[i];
+    if (!t.ptr) continue;
+    if (i == 4 && a->variant == GDR_GDN) continue;  // scalar gate: element access
+    const int es = elem_size(t.dtype);
+    if (reinterpret_cast<uintptr_t>(t.ptr) % 16 || (t.stride_b * es) % 16 || (t.stride_h * es) % 16 ||
+        (t.stride_t * es) % 16)
+      return fail(GDR_ERR_INVALID, "%s: base pointer and b/h/t strides must be 16-byte aligned", names[i]);
+  }
+  const int64_t need = gdr::chunk_workspace_bytes(*a);
+  hipError_t e;
+  if (a->workspace) {
+    if (a->workspace_bytes < need)
+      return fail(GDR_ERR_INVALID, "workspace of %lld bytes given, %lld required", (long long)a->workspace_bytes,
+                  (long long)need);
+    if (reinterpret_cast<uintptr_t>(a->workspace) % 256)
+      return fail(GDR_ERR_INVALID, "workspace must be 256-byte aligned");
+    e = gdr::launch_chunk_split(*a, pro ? *pro : gdr_prologue{}, stream);
+  } else {
+    e = gdr::launch_chunk(*a, stream);
+  }
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "chunk launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
   return GDR_OK;
 }
 
@@ -143,39 +209,11 @@ int64_t gdr_chunk_workspace_bytes(const gdr_args* a) {
   return gdr::chunk_workspace_bytes(*a);
 }
 
-int gdr_chunk_fwd(const gdr_args* a, hipStream_t stream) {
-  int rc = check_common(a, true);
-  if (rc) return rc;
-  if (a->q.dtype != GDR_BF16 || a->k.dtype != GDR_BF16 || a->v.dtype != GDR_BF16)
-    return fail(GDR_ERR_UNSUPPORTED, "chunk mode reads bf16 q, k, v (got dtype codes %d, %d, %d)", a->q.dtype,
-                a->k.dtype, a->v.dtype);
-  // Rows of q, k, v, gate and out are moved with 16-byte accesses.
-  const gdr_tensor* rows[] = {&a->q, &a->k, &a->v, &a->out, &a->gate};
-  const char* names[] = {"query", "key", "value", "out", "gate"};
-  for (int i = 0; i < 5; ++i) {
-    const gdr_tensor& t = *rows[i];
-    if (!t.ptr) continue;
-    if (i == 4 && a->variant == GDR_GDN) continue;  // scalar gate: element access
-    const int es = elem_size(t.dtype);
-    if (reinterpret_cast<uintptr_t>(t.ptr) % 16 || (t.stride_b * es) % 16 || (t.stride_h * es) % 16 ||
-        (t.stride_t * es) % 16)
-      return fail(GDR_ERR_INVALID, "%s: base pointer and b/h/t strides must be 16-byte aligned", names[i]);
-  }
-  const int64_t need = gdr::chunk_workspace_bytes(*a);
-  hipError_t e;
-  if (a->workspace) {
-    if (a->workspace_bytes < need)
-      return fail(GDR_ERR_INVALID, "workspace of %lld bytes given, %lld required", (long long)a->workspace_bytes,
-                  (long long)need);
-    if (reinterpret_cast<uintptr_t>(a->workspace) % 256)
-      return fail(GDR_ERR_INVALID, "workspace must be 256-byte aligned");
-    e = gdr::launch_chunk_split(*a, stream);
-  } else {
-    e = gdr::launch_chunk(*a, stream);
-  }
-  if (e != hipSuccess) return fail(GDR_ERR_HIP, "chunk launch failed: %s", hipGetErrorString(e));
-  g_last_error.clear();
-  return GDR_OK;
+int gdr_chunk_fwd(const gdr_args* a, hipStream_t stream) { return chunk_fwd(a, nullptr, stream); }
+
+int gdr_chunk_fwd_fused(const gdr_args* a, const gdr_prologue* pro, hipStream_t stream) {
+  if (!pro) return fail(GDR_ERR_INVALID, "prologue is NULL");
+  return chunk_fwd(a, pro, stream);
 }
 
 int64_t gdr_chunk_bwd_workspace_bytes(const gdr_args* a) {

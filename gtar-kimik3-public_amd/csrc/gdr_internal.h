@@ -22,8 +22,9 @@ hipError_t launch_chunk(const gdr_args& a, hipStream_t stream);
 
 // Chunkwise forward as a chunk-parallel preparation launch plus a state-scan launch over a workspace of
 // chunk_workspace_bytes(a) bytes at a.workspace.
+// `pro` is the fused layer prologue (flags 0 for the plain op).
 int64_t chunk_workspace_bytes(const gdr_args& a);
-hipError_t launch_chunk_split(const gdr_args& a, hipStream_t stream);
+hipError_t launch_chunk_split(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream);
 
 // Byte offsets of the chunkwise-backward buffers inside its workspace (each 256-aligned).  Per (sequence, head):
 //   rec      the forward records (chunk_workspace_bytes layout)

@@ -33,16 +33,6 @@ struct Rec {
   static __device__ __forceinline__ int rt(int row, int tok) { return row * 64 + (((tok >> 3) ^ (row & 7)) << 3) + (tok & 7); }
 };
 
-// Inclusive prefix sum over the 16 lanes of each DPP row (v_add_f32 with row_shr:1, 2, 4, 8; lanes shifted in from
-// outside the row contribute 0).
-__device__ __forceinline__ float row_scan16(float x) {
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, true));
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, true));
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, true));
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, true));
-  return x;
-}
-
 // Four consecutive outputs in one 8-byte (16-bit types) or 16-byte (fp32) store.
 __device__ __forceinline__ void store4(__bf16* dst, floatx4 v) {
   *reinterpret_cast<bf16x4*>(dst) = bf16x4{bf(v[0]), bf(v[1]), bf(v[2]), bf(v[3])};

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GDR_ABI_VERSION 4
+#define GDR_ABI_VERSION 5
 
 typedef enum gdr_variant { GDR_KDA = 0, GDR_GDN = 1, GDR_GLA = 2, GDR_DELTANET = 3 } gdr_variant;
 
@@ -87,6 +87,29 @@ typedef struct gdr_args {
  * operand type; the Python layer casts); out may be bf16, f16 or f32.
  * Supports K in {64, 128}, V a multiple of 64, any T >= 1, and packed varlen input through cu_seqlens. */
 int gdr_chunk_fwd(const gdr_args* args, hipStream_t stream);
+
+/* Fused layer prologue for gdr_chunk_fwd_fused: the per-token work the reference's KDA layer does in PyTorch before
+ * calling the op (src/layers/kimi_delta_attention.py:45-49), done inside the chunk-parallel preparation kernel
+ * instead, so the fp32 [B, T, H, K] gate and the normalised q, k never exist in HBM. */
+#define GDR_PRO_NORM_QK 1      /* q, k are L2-normalised per (token, head): x / max(||x||_2, 1e-12) (F.normalize) */
+#define GDR_PRO_BETA_LOGITS 2  /* beta holds logits; the kernel applies the sigmoid */
+#define GDR_PRO_GATE_LOWRANK 4 /* KDA, GLA: gate = -exp(a_log[h]) * softplus(z W[h]^T + bias[h]) in the kernel,
+                                  from the rank-R activations z of the gate's first projection; args->gate must
+                                  be NULL */
+typedef struct gdr_prologue {
+  int32_t flags;            /* GDR_PRO_* bits */
+  int32_t rank;             /* R: width of z, a multiple of 32 up to 512 (GATE_LOWRANK) */
+  gdr_tensor gate_lowrank;  /* z [B, T, R] bf16 (stride_h ignored; rows 16-byte aligned): decay_proj[0](x) */
+  const void* gate_weight;  /* [H * K, R] bf16 row-major, 16-byte aligned: decay_proj[1].weight */
+  const float* gate_bias;   /* [H * K] f32, 16-byte aligned, or NULL: decay_proj[1].bias */
+  const float* a_log;       /* [H] f32: A_log */
+} gdr_prologue;
+
+/* gdr_chunk_fwd with the fused prologue `pro`.  Replaces the layer-side q/k normalisation, beta sigmoid and gate
+ * computation of KimiDeltaAttention.forward (src/layers/kimi_delta_attention.py:45-49) plus the op call (:51-55).
+ * With GDR_PRO_NORM_QK, q and k are the un-normalised rows; with GDR_PRO_BETA_LOGITS, beta holds logits.  Needs a
+ * workspace (the two-launch path); other limits as gdr_chunk_fwd.  No backward: train through gdr_chunk_fwd. */
+int gdr_chunk_fwd_fused(const gdr_args* args, const gdr_prologue* pro, hipStream_t stream);
 
 /* Bytes of device workspace gdr_chunk_fwd needs for `args` (sizes, variant, key/value dims and varlen fields are
  * read; no pointer is dereferenced), or a negative gdr_status.  The workspace holds one record per (chunk, head)

@@ -23,13 +23,18 @@ Contents, each a restatement in this repository's own torch code of the referenc
 * `varlen`          -- packed variable-length input (`cu_seqlens`) as the concatenation of independent
                        per-sequence runs.  The reference has no varlen path; this is the definition the kernel is
                        held to.
+* `layer_prologue`  -- the KDA layer's preparation of the op's inputs (src/layers/kimi_delta_attention.py:45-49):
+                       F.normalize of q and k, beta = sigmoid(beta logits), and the gate
+                       -exp(A_log) * softplus(decay_proj[1](z)) from the rank-R activations z = decay_proj[0](x).
+                       The definition the fused-prologue kernel is held to.
 
 How each function is pinned (tests/test_oracle.py): closed forms (one-hot keys give an exact per-row
 overwrite / exponential-moving-average memory; beta = 0 gives pure decay of the initial state; GLA's
 non-recursive sum; DeltaNet with orthonormal keys and beta = 1 gives exact associative recall), the variant
 reductions (KDA with g = 0 is DeltaNet, KDA with channel-constant g is GDN, GLA with g = 0 is linear attention),
 chunkwise == recurrence at several chunk sizes, state passing between segments, causality, scale linearity and
-varlen == per-sequence runs.  No function is left "parity unpinned".
+varlen == per-sequence runs; `layer_prologue` against torch.nn.functional's normalize / softplus / sigmoid and
+nn.Linear (library routines).  No function is left "parity unpinned".
 
 Layouts follow the reference: q, k [B, H, T, K]; v [B, H, T, V]; gate [B, H, T, K] (KDA, GLA) or [B, H, T]
 (GDN); beta [B, H, T]; state [B, H, K, V].
@@ -171,3 +176,24 @@ def varlen(fn, variant, query, key, value, gate, beta, scale, initial_state, cu_
         outs.append(o)
         states.append(st)
     return torch.cat(outs, 2), torch.cat(states, 0)
+
+
+def layer_prologue(query, key, gate_lowrank, gate_weight, gate_bias, a_log, beta_logits=None, dtype=torch.float64):
+    """The KDA layer's input preparation (src/layers/kimi_delta_attention.py:45-49) in `dtype`.
+
+    q, k [B, H, T, K] (before normalisation); z = gate_lowrank [B, T, R]; gate_weight [H*K, R]; gate_bias [H*K] or
+    None; a_log [H]; beta_logits [B, H, T] or None.  Returns (q / max(|q|, 1e-12), k / max(|k|, 1e-12),
+    gate [B, H, T, K], beta) with gate[b, h, t, c] = -exp(a_log[h]) * softplus(z[b, t] . W[h K + c] + bias[h K + c])
+    (softplus(x) = x above 20, as torch's threshold) and beta = 1 / (1 + exp(-logits)).
+    """
+    q, k = query.to(dtype), key.to(dtype)
+    qn = q / q.pow(2).sum(-1, keepdim=True).sqrt().clamp_min(1e-12)
+    kn = k / k.pow(2).sum(-1, keepdim=True).sqrt().clamp_min(1e-12)
+    batch, heads, seq_len, key_dim = q.shape
+    x = torch.einsum("btr,nr->btn", gate_lowrank.to(dtype), gate_weight.to(dtype))
+    if gate_bias is not None:
+        x = x + gate_bias.to(dtype)
+    soft = torch.where(x > 20, x, torch.log1p(torch.exp(x.clamp_max(20))))
+    gate = -torch.exp(a_log.to(dtype))[:, None] * soft.view(batch, seq_len, heads, key_dim)
+    beta = None if beta_logits is None else 1.0 / (1.0 + torch.exp(-beta_logits.to(dtype)))
+    return qn, kn, gate.transpose(1, 2), beta

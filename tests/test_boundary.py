@@ -42,6 +42,8 @@ def test_struct_layout_matches_header(tmp_path):
     lines += [f'printf("t.{f} %zu\\n", offsetof(gdr_tensor, {f}));' for f, _ in lib.GdrTensor._fields_]
     lines += [f'printf("g.{f} %zu\\n", offsetof(gdr_grads, {f}));' for f, _ in lib.GdrGrads._fields_]
     lines += ['printf("g.size %zu\\n", sizeof(gdr_grads));']
+    lines += [f'printf("p.{f} %zu\\n", offsetof(gdr_prologue, {f}));' for f, _ in lib.GdrPrologue._fields_]
+    lines += ['printf("p.size %zu\\n", sizeof(gdr_prologue));']
     lines += ["return 0; }"]
     probe.write_text("\n".join(lines))
     exe = tmp_path / "layout"
@@ -58,6 +60,9 @@ def test_struct_layout_matches_header(tmp_path):
     for f, _ in lib.GdrGrads._fields_:
         assert int(offsets["g." + f]) == getattr(lib.GdrGrads, f).offset, f
     assert int(offsets["g.size"]) == ctypes.sizeof(lib.GdrGrads)
+    for f, _ in lib.GdrPrologue._fields_:
+        assert int(offsets["p." + f]) == getattr(lib.GdrPrologue, f).offset, f
+    assert int(offsets["p.size"]) == ctypes.sizeof(lib.GdrPrologue)
 
 
 def test_last_error_reports_invalid_arguments_without_a_gpu():
@@ -180,3 +185,44 @@ def test_recurrent_cache_accept_adopts_the_prefix_state():
     assert all(torch.equal(c, t) for c, t in zip(cache.conv_states, tails))
     with pytest.raises(RuntimeError):
         cache.rollback()
+
+
+def test_fused_prologue_rejects_bad_arguments_without_a_gpu():
+    so = lib.load_library()
+    args = lib.GdrArgs()
+    args.abi_version = lib.ABI_VERSION
+    args.variant, args.batch, args.heads, args.seq_len, args.key_dim, args.value_dim = 0, 1, 1, 64, 128, 128
+    for name, off in (("q", 256), ("k", 512), ("v", 768), ("out", 1024), ("beta", 1280)):
+        view = getattr(args, name)
+        view.ptr, view.dtype = off, lib.F32 if name == "beta" else lib.BF16
+    args.workspace, args.workspace_bytes = 4096, 1 << 30
+    assert so.gdr_chunk_fwd_fused(ctypes.byref(args), None, None) == -1
+    assert b"prologue" in so.gdr_last_error()
+    pro = lib.GdrPrologue()
+    pro.flags = 8
+    assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -1
+    assert b"flags" in so.gdr_last_error()
+    pro.flags = lib.PRO_GATE_LOWRANK
+    pro.rank = 48
+    assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -2
+    assert b"rank 48" in so.gdr_last_error()
+    pro.rank = 128
+    pro.gate_lowrank.ptr, pro.gate_lowrank.dtype, pro.gate_lowrank.stride_t = 2048, lib.BF16, 128
+    pro.gate_weight, pro.a_log = 8192, 16384
+    args.gate.ptr, args.gate.dtype = 1536, lib.F32  # the gate is computed: a gate tensor is an error
+    assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -1
+    assert b"computed" in so.gdr_last_error()
+    args.gate.ptr = None
+    args.variant = 1  # GDN has a scalar gate: no low-rank form
+    assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -2
+    assert b"per-channel" in so.gdr_last_error()
+
+
+def test_fused_prologue_refuses_gradients_and_cpu_tensors():
+    q, k, v, g, b = _cpu_inputs()
+    z, w, a_log = torch.randn(1, 8, 32), torch.randn(2 * 64, 32), torch.zeros(2)
+    with pytest.raises(ValueError, match="GPU"):
+        gdr.chunk_kimi_delta_attention_fused(q, k, v, z, w, None, a_log, b)
+    q.requires_grad_()
+    with pytest.raises(NotImplementedError, match="no backward"):
+        gdr.chunk_kimi_delta_attention_fused(q, k, v, z, w, None, a_log, b)

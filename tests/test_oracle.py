@@ -206,3 +206,32 @@ def test_kda_reference_dtype_contract():
                                      None, h0.float())
     assert (out.double() - ref_o).abs().max() <= 1e-2 * ref_o.abs().max()
     assert (state.double() - ref_s).norm() <= 1e-5 * ref_s.norm()
+
+
+def test_layer_prologue_matches_torch_functional():
+    """layer_prologue against the library routines the reference layer calls (F.normalize, nn.Linear, F.softplus,
+    sigmoid), including softplus's linear branch above 20 and a zero-norm row (the 1e-12 floor)."""
+    gen = torch.Generator().manual_seed(5)
+    B, H, T, K, R = 2, 3, 7, 8, 6
+    q = torch.randn(B, H, T, K, generator=gen, dtype=torch.float64)
+    k = torch.randn(B, H, T, K, generator=gen, dtype=torch.float64)
+    q[0, 0, 0] = 0.0
+    z = torch.randn(B, T, R, generator=gen, dtype=torch.float64)
+    w = torch.randn(H * K, R, generator=gen, dtype=torch.float64)
+    w[3] *= 40.0  # channel 3 of head 0 crosses softplus's threshold
+    bias = torch.randn(H * K, generator=gen, dtype=torch.float64)
+    a_log = torch.log(torch.empty(H, dtype=torch.float64).uniform_(1, 16, generator=gen))
+    logits = torch.randn(B, H, T, generator=gen, dtype=torch.float64)
+    qn, kn, gate, beta = oracle.layer_prologue(q, k, z, w, bias, a_log, logits)
+    lin = torch.nn.Linear(R, H * K, bias=True).double()
+    with torch.no_grad():
+        lin.weight.copy_(w)
+        lin.bias.copy_(bias)
+        raw = lin(z)
+    ref_gate = (-a_log.exp()[:, None] * F.softplus(raw.view(B, T, H, K))).transpose(1, 2)
+    assert (raw > 20).any()
+    torch.testing.assert_close(gate, ref_gate, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(qn, F.normalize(q, dim=-1), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(kn, F.normalize(k, dim=-1), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(beta, torch.sigmoid(logits), rtol=1e-12, atol=1e-12)
+    assert torch.count_nonzero(qn[0, 0, 0]) == 0
