@@ -18,7 +18,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.join(_HERE, "libgdr.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 PRO_NORM_QK, PRO_BETA_LOGITS, PRO_GATE_LOWRANK = 1, 2, 4
 
 KDA, GDN, GLA, DELTANET = 0, 1, 2, 3
@@ -74,6 +74,43 @@ class GdrPrologue(ctypes.Structure):
     ]
 
 
+class GdrAttentionArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("kv_heads", ctypes.c_int32),
+        ("seq_len", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("n_seqs", ctypes.c_int32),
+        ("q", GdrTensor),
+        ("k", GdrTensor),
+        ("v", GdrTensor),
+        ("out", GdrTensor),
+        ("cu_seqlens", ctypes.c_void_p),
+    ]
+
+
+class GdrConvArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("seq_len", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("kernel_size", ctypes.c_int32),
+        ("n_seqs", ctypes.c_int32),
+        ("apply_silu", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("x", GdrTensor),
+        ("out", GdrTensor),
+        ("weight", ctypes.c_void_p),
+        ("state_in", ctypes.c_void_p),
+        ("state_out", ctypes.c_void_p),
+        ("cu_seqlens", ctypes.c_void_p),
+    ]
+
+
 class GdrGrads(ctypes.Structure):
     _fields_ = [
         ("d_out", GdrTensor),
@@ -99,6 +136,8 @@ EXPORTS = {
     "gdr_recurrent_verify": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p]),
     "gdr_recurrent_commit": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p,
                                             ctypes.c_void_p]),
+    "gdr_attention_fwd": (ctypes.c_int, [ctypes.POINTER(GdrAttentionArgs), ctypes.c_void_p]),
+    "gdr_short_conv_fwd": (ctypes.c_int, [ctypes.POINTER(GdrConvArgs), ctypes.c_void_p]),
     "gdr_last_error": (ctypes.c_char_p, []),
     "gdr_abi_version": (ctypes.c_int, []),
 }
@@ -256,3 +295,48 @@ def launch_fused(args: GdrArgs, pro: GdrPrologue, device: torch.device) -> None:
     stream = torch.cuda.current_stream(device).cuda_stream
     _check("gdr_chunk_fwd_fused", lib.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro),
                                                           ctypes.c_void_p(stream)))
+
+
+def _view3(x: torch.Tensor, name: str) -> GdrTensor:
+    """[B, T, C] view (stride_h unused)."""
+    if x.dtype not in _DTYPE_CODES:
+        raise TypeError(f"{name}: unsupported dtype {x.dtype}")
+    view = GdrTensor()
+    view.ptr, view.dtype = x.data_ptr(), _DTYPE_CODES[x.dtype]
+    view.stride_b, view.stride_h, view.stride_t = x.stride(0), 0, x.stride(1)
+    return view
+
+
+def attention(q, k, v, out, scale, cu_seqlens, device) -> None:
+    """Enqueue gdr_attention_fwd on torch's current stream."""
+    args = GdrAttentionArgs()
+    args.abi_version = ABI_VERSION
+    args.batch, args.heads, args.seq_len, args.head_dim = q.shape[0], q.shape[1], q.shape[2], q.shape[3]
+    args.kv_heads = k.shape[1]
+    args.scale = float(scale)
+    args.q, args.k, args.v, args.out = _view(q, "query"), _view(k, "key"), _view(v, "value"), _view(out, "out")
+    if cu_seqlens is not None:
+        args.cu_seqlens = cu_seqlens.data_ptr()
+        args.n_seqs = cu_seqlens.numel() - 1
+    lib = load_library()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    _check("gdr_attention_fwd", lib.gdr_attention_fwd(ctypes.byref(args), ctypes.c_void_p(stream)))
+
+
+def short_conv(x, out, weight, state_in, state_out, cu_seqlens, silu, device) -> None:
+    """Enqueue gdr_short_conv_fwd on torch's current stream."""
+    args = GdrConvArgs()
+    args.abi_version = ABI_VERSION
+    args.batch, args.seq_len, args.channels = x.shape
+    args.kernel_size = weight.shape[-1]
+    args.apply_silu = int(bool(silu))
+    args.x, args.out = _view3(x, "x"), _view3(out, "out")
+    args.weight = weight.data_ptr()
+    args.state_in = state_in.data_ptr() if state_in is not None else None
+    args.state_out = state_out.data_ptr() if state_out is not None else None
+    if cu_seqlens is not None:
+        args.cu_seqlens = cu_seqlens.data_ptr()
+        args.n_seqs = cu_seqlens.numel() - 1
+    lib = load_library()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    _check("gdr_short_conv_fwd", lib.gdr_short_conv_fwd(ctypes.byref(args), ctypes.c_void_p(stream)))

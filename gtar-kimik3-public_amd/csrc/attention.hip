@@ -1,0 +1,264 @@
+// Causal softmax attention (grouped-query, optional packed variable-length input) on gfx950 -- the attention layer
+// of the hybrid stack (src/layers/attention.py:82-117, src/ops/flash_attention_2.py:24-151, forward only).
+//
+//   O[t] = sum_{s <= t} softmax_s(scale q_t . k_s) v_s       per (sequence, query head); key/value head h / (H / Hkv)
+//
+// One 512-thread workgroup owns 128 query rows of one (sequence, query head); wave w owns rows 16 w .. 16 w + 15.
+// Key/value tiles of 64 rows stream through double-buffered LDS (K and V rows XOR-swizzled by 16-byte chunk), loaded
+// straight into LDS (no registers) while the current tile is used.  Per tile and wave, on
+// v_mfma_f32_16x16x32_{bf16,f16}:
+//   * S^T = K Q^T  -- K rows from LDS as A, the wave's Q rows (registers for the whole call) as B, so each lane holds
+//     16 scores of one query row (lane % 16) and the online-softmax statistics stay per lane;
+//   * O^T += V^T P^T -- V^T through the transposing LDS read (ds_read_b64_tr_b16) as A, the bf16/f16 probabilities
+//     straight from the score registers as B (the key order inside a 32-key step is the one the score tiles give;
+//     the V^T read follows it), so O^T lands in the same per-query-row lane layout.
+// Scores are scaled into log2 units and exponentiated with v_exp_f32; fully masked tiles are computed and masked
+// (no MFMA sits under a data-dependent branch).
+#include "chunk_common.h"
+#include "gdr_internal.h"
+
+namespace gdr {
+namespace {
+
+using chunk::kLog2e;
+using chunk::lds_read_tr;
+using chunk::pack4;
+
+constexpr int kBM = 128;  // query rows per workgroup
+constexpr int kBN = 64;   // keys per LDS tile
+constexpr int kAttnThreads = 512;
+constexpr float kNegInf = -__builtin_inff();
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Mma;
+template <>
+struct Mma<__bf16> {
+  using v8 = bf16x8;
+  using v4 = bf16x4;
+  static __device__ __forceinline__ floatx4 run(v8 a, v8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ v4 pack(floatx4 x) { return pack4(x); }
+};
+template <>
+struct Mma<_Float16> {
+  using v8 = f16x8;
+  using v4 = f16x4;
+  static __device__ __forceinline__ floatx4 run(v8 a, v8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ v4 pack(floatx4 x) {
+    return v4{static_cast<_Float16>(x[0]), static_cast<_Float16>(x[1]), static_cast<_Float16>(x[2]),
+              static_cast<_Float16>(x[3])};
+  }
+};
+
+template <typename V4, typename V8>
+__device__ __forceinline__ V8 cat(V4 lo, V4 hi) {
+  return V8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// 16 bytes from global memory straight into LDS (global_load_lds_dwordx4): lane i's bytes land at the wave-uniform
+// LDS address `lds_base` + 16 i.
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+// First query-block slot of packed sequence n: floor(bos / kBM) + n (slots of consecutive sequences never overlap).
+__device__ __forceinline__ int attn_slot_base(const int32_t* cu, int n) { return cu[n] / kBM + n; }
+
+template <int D, typename T>
+__global__ __launch_bounds__(kAttnThreads, 4) void attention_fwd_kernel(const gdr_attention_args a, int nqb) {
+  using M = Mma<T>;
+  using V8 = typename M::v8;
+  using V4 = typename M::v4;
+  constexpr int DC = D / 8;         // 16-byte chunks per row
+  constexpr int DS = D / 32;        // 32-wide k steps of S^T = K Q^T
+  constexpr int DT = D / 16;        // 16-column tiles of O^T
+  constexpr int TILE = kBN * D;     // elements per K or V tile
+  constexpr int LOADS = kBN * DC / kAttnThreads;  // 16-byte pieces per thread per tile
+  static_assert(LOADS >= 1 && kBN * DC % kAttnThreads == 0, "tile load split");
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* ks = reinterpret_cast<T*>(smem);              // [2][kBN][D] swizzled
+  T* vs = reinterpret_cast<T*>(smem) + 2 * TILE;   // [2][kBN][D] swizzled
+
+  // ---- workgroup -> (sequence, query block, head); the latest query blocks (the most keys) are dispatched first ----
+  const int H = a.heads;
+  const int h = blockIdx.x % H, slot = blockIdx.x / H;
+  int n, qb, bos = 0, len = a.seq_len;
+  if (a.cu_seqlens) {
+    int lo = 0, hi = a.n_seqs - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (attn_slot_base(a.cu_seqlens, mid) <= slot) lo = mid; else hi = mid - 1;
+    }
+    n = lo;
+    bos = a.cu_seqlens[n];
+    len = a.cu_seqlens[n + 1] - bos;
+    const int nb = (len + kBM - 1) / kBM;
+    const int r = slot - attn_slot_base(a.cu_seqlens, n);
+    if (r < 0 || r >= nb) return;  // gap slot: uniform over the workgroup, before any barrier
+    qb = nb - 1 - r;
+  } else {
+    n = slot / nqb;
+    qb = nqb - 1 - slot % nqb;
+  }
+  const int bidx = a.cu_seqlens ? 0 : n;
+  const int hk = h / (H / a.kv_heads);
+  const T* qp = static_cast<const T*>(a.q.ptr) + bidx * a.q.stride_b + h * a.q.stride_h + int64_t(bos) * a.q.stride_t;
+  const T* kp = static_cast<const T*>(a.k.ptr) + bidx * a.k.stride_b + hk * a.k.stride_h + int64_t(bos) * a.k.stride_t;
+  const T* vp = static_cast<const T*>(a.v.ptr) + bidx * a.v.stride_b + hk * a.v.stride_h + int64_t(bos) * a.v.stride_t;
+  T* op = static_cast<T*>(const_cast<void*>(a.out.ptr)) + bidx * a.out.stride_b + h * a.out.stride_h +
+          int64_t(bos) * a.out.stride_t;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, g4 = lane >> 4;
+  const int q0 = qb * kBM;
+  const int qpos = q0 + 16 * wave + l16;  // this lane's query row (position in the sequence)
+  const int qrow = min(qpos, len - 1);
+
+  // Q rows as the B operand of S^T = K Q^T: lane (l16, g4) holds q[qpos][32 ds + 8 g4 .. + 7].
+  V8 qf[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) qf[ds] = *reinterpret_cast<const V8*>(qp + int64_t(qrow) * a.q.stride_t + 32 * ds + 8 * g4);
+
+  // ---- key/value tiles: global -> LDS directly (global_load_lds_dwordx4: a lane's 16 bytes land at the wave-
+  // uniform LDS base + 16 * lane).  Row r, chunk c of a tile is stored at chunk c ^ (r mod DC), so each lane loads
+  // the global chunk that belongs at its LDS slot. ----
+  const int kend = min(len, q0 + kBM);  // keys this block can see
+  const int nkb = (kend + kBN - 1) / kBN;
+  constexpr int GROUPS = kBN * DC / kWave;  // 64-piece groups per tile
+  constexpr int kWaves = kAttnThreads / kWave;
+  static_assert((2 * GROUPS) % kWaves == 0, "tile groups per wave");
+  auto issue_tile = [&](int kb, int buf) {
+#pragma unroll
+    for (int k = 0; k < 2 * GROUPS / kWaves; ++k) {
+      const int g = wave + kWaves * k;
+      const bool is_v = g >= GROUPS;
+      const int gg = is_v ? g - GROUPS : g;
+      const int slot = kWave * gg + lane, row = slot / DC, cc = (slot % DC) ^ (row % DC);
+      const int64_t key = min(kb * kBN + row, len - 1);
+      const T* src = is_v ? vp + key * a.v.stride_t + 8 * cc : kp + key * a.k.stride_t + 8 * cc;
+      T* dst = (is_v ? vs : ks) + buf * TILE + kWave * 8 * gg;
+      lds_dma16(src, dst);
+    }
+  };
+
+  const float c = a.scale * kLog2e;  // scores in log2 units
+  float m = kNegInf, l = 0.f;      // running max (log2 units) and sum for this lane's query row
+  floatx4 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  issue_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {  // the accumulators start at zero right before this loop
+    const int buf = kb & 1;
+    if (kb + 1 < nkb) issue_tile(kb + 1, buf ^ 1);  // every wave is done with that buffer (tile kb - 1)
+    const T* kt = ks + buf * TILE;
+
+    // S^T tiles: lane holds S[qpos][kb * kBN + 16 t + 4 g4 + i]
+    floatx4 s[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      const int row = 16 * t + l16;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        const V8 kf = *reinterpret_cast<const V8*>(kt + row * D + (((4 * ds + g4) ^ (row % DC)) << 3));
+        s[t] = M::run(kf, qf[ds], s[t]);
+      }
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kb * kBN + 16 * t + 4 * g4 + i;
+        s[t][i] = key <= qpos && key < len ? s[t][i] * c : kNegInf;
+        mx = fmaxf(mx, s[t][i]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(m, mx);
+    const float base = m_new == kNegInf ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m - base);
+    float rs = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[t][i] = __builtin_amdgcn_exp2f(s[t][i] - base);
+        rs += s[t][i];
+      }
+    rs += __shfl_xor(rs, 16, kWave);
+    rs += __shfl_xor(rs, 32, kWave);
+    l = l * alpha + rs;
+    m = m_new;
+    V8 pf[2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) pf[s2] = cat<V4, V8>(M::pack(s[2 * s2]), M::pack(s[2 * s2 + 1]));
+
+    // O^T += V^T P^T: V^T rows 32 s2 + 4 g4 + r (and + 16), column 16 t + l16, through the transposing read
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[t][i] *= alpha;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int col = 16 * t + 4 * (l16 & 3);
+        const int r0 = 32 * s2 + 4 * g4 + (l16 >> 2), r1 = r0 + 16;
+        const int off0 = buf * TILE + r0 * D + (((col >> 3) ^ (r0 % DC)) << 3) + (col & 7);
+        const int off1 = buf * TILE + r1 * D + (((col >> 3) ^ (r1 % DC)) << 3) + (col & 7);
+        const V4 lo = __builtin_bit_cast(V4, lds_read_tr(reinterpret_cast<const unsigned char*>(vs), off0 * 2));
+        const V4 hi = __builtin_bit_cast(V4, lds_read_tr(reinterpret_cast<const unsigned char*>(vs), off1 * 2));
+        o[t] = M::run(cat<V4, V8>(lo, hi), pf[s2], o[t]);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile kb + 1 have landed
+    __syncthreads();                 // ... everyone's, and every wave is done with tile kb
+  }
+
+  if (qpos < len) {
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      floatx4 y = o[t];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] *= inv;
+      *reinterpret_cast<V4*>(op + int64_t(qpos) * a.out.stride_t + 16 * t + 4 * g4) = M::pack(y);
+    }
+  }
+}
+
+template <int D, typename T>
+hipError_t launch_attention_typed(const gdr_attention_args& a, hipStream_t stream) {
+  constexpr int lds = 4 * kBN * D * 2;  // K and V, double-buffered
+  static bool configured = false;       // benign race: every thread sets the same attribute
+  if (!configured) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_fwd_kernel<D, T>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const int nqb = (a.seq_len + kBM - 1) / kBM;
+  const int64_t slots = a.cu_seqlens ? int64_t(nqb) + a.n_seqs : int64_t(a.batch) * nqb;
+  if (slots * a.heads > 0)
+    hipLaunchKernelGGL((attention_fwd_kernel<D, T>), dim3(unsigned(slots * a.heads)), dim3(kAttnThreads), lds, stream,
+                       a, nqb);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_attention(const gdr_attention_args& a, hipStream_t stream) {
+  if (a.q.dtype == GDR_BF16)
+    return a.head_dim == 64 ? launch_attention_typed<64, __bf16>(a, stream) : launch_attention_typed<128, __bf16>(a, stream);
+  return a.head_dim == 64 ? launch_attention_typed<64, _Float16>(a, stream)
+                          : launch_attention_typed<128, _Float16>(a, stream);
+}
+
+}  // namespace gdr

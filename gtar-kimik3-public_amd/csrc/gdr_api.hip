@@ -202,6 +202,63 @@ int gdr_recurrent_commit(const gdr_args* a, const float* updates, const int32_t*
   return GDR_OK;
 }
 
+int gdr_attention_fwd(const gdr_attention_args* a, hipStream_t stream) {
+  if (!a) return fail(GDR_ERR_INVALID, "args is NULL");
+  if (a->abi_version != GDR_ABI_VERSION)
+    return fail(GDR_ERR_INVALID, "abi_version %d, library implements %d", a->abi_version, GDR_ABI_VERSION);
+  if (a->batch < 1 || a->heads < 1 || a->kv_heads < 1 || a->seq_len < 0)
+    return fail(GDR_ERR_INVALID, "bad sizes B=%d H=%d Hkv=%d T=%d", a->batch, a->heads, a->kv_heads, a->seq_len);
+  if (a->heads % a->kv_heads) return fail(GDR_ERR_INVALID, "kv_heads %d does not divide heads %d", a->kv_heads, a->heads);
+  if (a->head_dim != 64 && a->head_dim != 128)
+    return fail(GDR_ERR_UNSUPPORTED, "head dim %d not supported (64 or 128)", a->head_dim);
+  if (a->cu_seqlens && (a->batch != 1 || a->n_seqs < 1))
+    return fail(GDR_ERR_INVALID, "cu_seqlens requires batch == 1 and n_seqs >= 1");
+  int rc;
+  const gdr_tensor* views[] = {&a->q, &a->k, &a->v, &a->out};
+  const char* names[] = {"query", "key", "value", "out"};
+  for (int i = 0; i < 4; ++i) {
+    if ((rc = check_view(*views[i], names[i], true, false))) return rc;
+    if (views[i]->dtype != a->q.dtype)
+      return fail(GDR_ERR_UNSUPPORTED, "%s: q, k, v and out share one dtype", names[i]);
+    if ((rc = check_rows16(*views[i], names[i]))) return rc;
+  }
+  if (a->q.dtype == GDR_F32) return fail(GDR_ERR_UNSUPPORTED, "attention reads bf16 or f16 (the MFMA operand types)");
+  hipError_t e = gdr::launch_attention(*a, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "attention launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
+int gdr_short_conv_fwd(const gdr_conv_args* a, hipStream_t stream) {
+  if (!a) return fail(GDR_ERR_INVALID, "args is NULL");
+  if (a->abi_version != GDR_ABI_VERSION)
+    return fail(GDR_ERR_INVALID, "abi_version %d, library implements %d", a->abi_version, GDR_ABI_VERSION);
+  if (a->batch < 1 || a->seq_len < 0 || a->channels < 1)
+    return fail(GDR_ERR_INVALID, "bad sizes B=%d T=%d C=%d", a->batch, a->seq_len, a->channels);
+  if (a->kernel_size < 2 || a->kernel_size > 8)
+    return fail(GDR_ERR_UNSUPPORTED, "kernel size %d not supported (2 to 8)", a->kernel_size);
+  if (a->cu_seqlens && (a->batch != 1 || a->n_seqs < 1))
+    return fail(GDR_ERR_INVALID, "cu_seqlens requires batch == 1 and n_seqs >= 1");
+  int rc;
+  if ((rc = check_view(a->x, "x", true, false)) || (rc = check_view(a->out, "out", true, false))) return rc;
+  if (a->out.dtype != a->x.dtype) return fail(GDR_ERR_UNSUPPORTED, "out must have x's dtype");
+  const int vec = 16 / elem_size(a->x.dtype);
+  if (a->channels % vec) return fail(GDR_ERR_UNSUPPORTED, "channels must be a multiple of %d", vec);
+  const gdr_tensor* rows[] = {&a->x, &a->out};
+  const char* names[] = {"x", "out"};
+  for (int i = 0; i < 2; ++i) {
+    const int es = elem_size(rows[i]->dtype);
+    if (reinterpret_cast<uintptr_t>(rows[i]->ptr) % 16 || (rows[i]->stride_b * es) % 16 || (rows[i]->stride_t * es) % 16)
+      return fail(GDR_ERR_INVALID, "%s: base pointer and b/t strides must be 16-byte aligned", names[i]);
+  }
+  if (!a->weight) return fail(GDR_ERR_INVALID, "weight: null pointer");
+  if (a->state_out && a->state_out == a->state_in) return fail(GDR_ERR_INVALID, "state_out must not alias state_in");
+  hipError_t e = gdr::launch_short_conv(*a, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "short convolution launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
 int64_t gdr_chunk_workspace_bytes(const gdr_args* a) {
   const int rc = check_shape(a, true);
   if (rc) return rc;

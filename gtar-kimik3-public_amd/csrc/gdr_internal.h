@@ -22,6 +22,10 @@ hipError_t launch_chunk(const gdr_args& a, hipStream_t stream);
 
 // Chunkwise forward as a chunk-parallel preparation launch plus a state-scan launch over a workspace of
 // chunk_workspace_bytes(a) bytes at a.workspace.
+// Causal grouped-query attention and the segment-aware short convolution; arguments validated.
+hipError_t launch_attention(const gdr_attention_args& a, hipStream_t stream);
+hipError_t launch_short_conv(const gdr_conv_args& a, hipStream_t stream);
+
 // `pro` is the fused layer prologue (flags 0 for the plain op).
 int64_t chunk_workspace_bytes(const gdr_args& a);
 hipError_t launch_chunk_split(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream);

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GDR_ABI_VERSION 5
+#define GDR_ABI_VERSION 6
 
 typedef enum gdr_variant { GDR_KDA = 0, GDR_GDN = 1, GDR_GLA = 2, GDR_DELTANET = 3 } gdr_variant;
 
@@ -178,6 +178,53 @@ int gdr_recurrent_verify(const gdr_args* args, float* updates, hipStream_t strea
  * Replaces RecurrentCache.commit / rollback plus the replay forward of the accepted prefix
  * (src/cache.py:59-86, src/speculative.py:397, 425-449). */
 int gdr_recurrent_commit(const gdr_args* args, const float* updates, const int32_t* accepted, hipStream_t stream);
+
+/* Causal softmax attention of the hybrid stack's attention layer (grouped-query; forward only). */
+typedef struct gdr_attention_args {
+  int32_t abi_version;       /* must equal GDR_ABI_VERSION */
+  int32_t batch;             /* B; must be 1 when cu_seqlens is given */
+  int32_t heads;             /* query heads H */
+  int32_t kv_heads;          /* key/value heads; divides H (query head h reads key/value head h / (H / kv_heads)) */
+  int32_t seq_len;           /* T (total packed length when cu_seqlens is given) */
+  int32_t head_dim;          /* D: 64 or 128 */
+  float scale;               /* softmax scale; the Python layer resolves `softmax_scale or D ** -0.5` */
+  int32_t n_seqs;            /* number of packed sequences; ignored when cu_seqlens is NULL */
+  gdr_tensor q, k, v;        /* [B, H, T, D] and [B, kv_heads, T, D] views, one dtype (bf16 or f16), rows 16-byte
+                                aligned */
+  gdr_tensor out;            /* [B, H, T, D], the dtype of q */
+  const int32_t* cu_seqlens; /* device int32 [n_seqs + 1] packed-sequence offsets, or NULL */
+} gdr_attention_args;
+
+/* O = softmax(scale Q K^T + causal mask) V per (sequence, query head), with attention confined to each packed
+ * sequence when cu_seqlens is given.  Replaces the forward of FlashAttention (src/ops/flash_attention_2.py:161-179,
+ * kernel :24-71, reached from src/layers/attention.py:113), which takes no packed input: the reference pads
+ * batches (flash_attention_2.py:155-158).  Supports D in {64, 128}, any T >= 1. */
+int gdr_attention_fwd(const gdr_attention_args* args, hipStream_t stream);
+
+/* Depthwise causal convolution + SiLU of the layers' short convolution, segment-aware. */
+typedef struct gdr_conv_args {
+  int32_t abi_version;       /* must equal GDR_ABI_VERSION */
+  int32_t batch;             /* B; must be 1 when cu_seqlens is given */
+  int32_t seq_len;           /* T (total packed length when cu_seqlens is given) */
+  int32_t channels;          /* C */
+  int32_t kernel_size;       /* W, 2 to 8 */
+  int32_t n_seqs;            /* number of packed sequences; ignored when cu_seqlens is NULL */
+  int32_t apply_silu;        /* nonzero: out = silu(conv(x)) (the layer's form); zero: out = conv(x) */
+  int32_t reserved;
+  gdr_tensor x;              /* [B, T, C] view (stride_h ignored), channels contiguous */
+  gdr_tensor out;            /* [B, T, C] view, channels contiguous */
+  const void* weight;        /* [C, W] in x's dtype: nn.Conv1d(C, C, W, groups=C).weight viewed as [C, W] */
+  const void* state_in;      /* [N, C, W - 1] in x's dtype: the W - 1 inputs before each sequence, or NULL (zeros) */
+  void* state_out;           /* [N, C, W - 1]: the last W - 1 inputs of each sequence after the call, or NULL; must
+                                not alias state_in */
+  const int32_t* cu_seqlens; /* device int32 [n_seqs + 1], or NULL (N = B) */
+} gdr_conv_args;
+
+/* out[t, c] = act(sum_{j < W} weight[c, j] x[t - W + 1 + j, c]), where inputs before a sequence's first token come
+ * from state_in (or are zero) -- never from the previous packed sequence.  Replaces ShortConvolution.forward
+ * (src/layers/short_convolution.py:11-20), whose padded conv runs across the batch layout and has no notion of packed
+ * sequences (:9, :15), including its conv-state path (:16-19). */
+int gdr_short_conv_fwd(const gdr_conv_args* args, hipStream_t stream);
 
 /* Thread-local description of the calling thread's last failure ("" if none).  No reference counterpart:
  * the reference surfaces failures as Python exceptions raised by Triton. */

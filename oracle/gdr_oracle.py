@@ -27,6 +27,10 @@ Contents, each a restatement in this repository's own torch code of the referenc
                        F.normalize of q and k, beta = sigmoid(beta logits), and the gate
                        -exp(A_log) * softplus(decay_proj[1](z)) from the rank-R activations z = decay_proj[0](x).
                        The definition the fused-prologue kernel is held to.
+* `causal_attention` -- causal grouped-query softmax attention (src/ops/flash_attention_2.py:24-71 forward,
+                       the SDPA fallback :220-221), confined to each packed sequence when `cu_seqlens` is given.
+* `short_convolution` -- depthwise causal convolution + SiLU (src/layers/short_convolution.py:11-20), including
+                       the conv-state path (:16-19), per packed sequence when `cu_seqlens` is given.
 
 How each function is pinned (tests/test_oracle.py): closed forms (one-hot keys give an exact per-row
 overwrite / exponential-moving-average memory; beta = 0 gives pure decay of the initial state; GLA's
@@ -34,7 +38,9 @@ non-recursive sum; DeltaNet with orthonormal keys and beta = 1 gives exact assoc
 reductions (KDA with g = 0 is DeltaNet, KDA with channel-constant g is GDN, GLA with g = 0 is linear attention),
 chunkwise == recurrence at several chunk sizes, state passing between segments, causality, scale linearity and
 varlen == per-sequence runs; `layer_prologue` against torch.nn.functional's normalize / softplus / sigmoid and
-nn.Linear (library routines).  No function is left "parity unpinned".
+nn.Linear, `causal_attention` against F.scaled_dot_product_attention (is_causal, enable_gqa) and
+`short_convolution` against nn.Conv1d / F.conv1d as the reference module calls them (library routines), each also
+per packed sequence.  No function is left "parity unpinned".
 
 Layouts follow the reference: q, k [B, H, T, K]; v [B, H, T, V]; gate [B, H, T, K] (KDA, GLA) or [B, H, T]
 (GDN); beta [B, H, T]; state [B, H, K, V].
@@ -197,3 +203,52 @@ def layer_prologue(query, key, gate_lowrank, gate_weight, gate_bias, a_log, beta
     gate = -torch.exp(a_log.to(dtype))[:, None] * soft.view(batch, seq_len, heads, key_dim)
     beta = None if beta_logits is None else 1.0 / (1.0 + torch.exp(-beta_logits.to(dtype)))
     return qn, kn, gate.transpose(1, 2), beta
+
+
+def causal_attention(query, key, value, scale=None, cu_seqlens=None, dtype=torch.float64):
+    """softmax(scale q k^T + causal mask) v per (sequence, query head) in `dtype`; query head h reads key/value head
+    h // (H / Hkv).  q [B, H, T, D], k and v [B, Hkv, T, D]; with `cu_seqlens` (batch 1) each packed sequence attends
+    only within itself.  Returns [B, H, T, D] in `dtype`."""
+    scale = scale or query.shape[-1] ** -0.5
+    q, k, v = (x.to(dtype) for x in (query, key, value))
+    heads, kv_heads = q.shape[1], k.shape[1]
+    group = heads // kv_heads
+    k = k.repeat_interleave(group, dim=1)
+    v = v.repeat_interleave(group, dim=1)
+    bounds = [0, q.shape[2]] if cu_seqlens is None else [int(x) for x in cu_seqlens]
+    out = torch.zeros_like(q)
+    for start, end in zip(bounds[:-1], bounds[1:]):
+        if end == start:
+            continue
+        qs, ks, vs = q[:, :, start:end], k[:, :, start:end], v[:, :, start:end]
+        scores = scale * qs @ ks.transpose(-1, -2)
+        mask = torch.ones(end - start, end - start, dtype=torch.bool).tril()
+        scores = scores.masked_fill(~mask, float("-inf"))
+        weights = torch.softmax(scores, dim=-1)
+        out[:, :, start:end] = weights @ vs
+    return out
+
+
+def short_convolution(x, weight, conv_state=None, cu_seqlens=None, activation=True, dtype=torch.float64):
+    """out[t, c] = act(sum_{j < W} weight[c, j] x[t - W + 1 + j, c]) per sequence, with the inputs before a
+    sequence from its conv state [N, C, W - 1] (zeros without one).  x [B, T, C] (batch 1 with `cu_seqlens`),
+    weight [C, 1, W] or [C, W].  Returns (out [B, T, C], new state [N, C, W - 1]) in `dtype`: the new state holds each
+    sequence's last W - 1 inputs (reaching into the old state for sequences shorter than W - 1)."""
+    xs = x.to(dtype)
+    w = weight.reshape(weight.shape[0], -1).to(dtype)
+    width = w.shape[1]
+    batch, seq_len, channels = xs.shape
+    bounds = [(b, 0, seq_len) for b in range(batch)] if cu_seqlens is None else \
+        [(0, int(cu_seqlens[n]), int(cu_seqlens[n + 1])) for n in range(len(cu_seqlens) - 1)]
+    out = torch.zeros_like(xs)
+    new_state = torch.zeros(len(bounds), channels, width - 1, dtype=dtype)
+    for n, (b, start, end) in enumerate(bounds):
+        prev = (torch.zeros(channels, width - 1, dtype=dtype) if conv_state is None
+                else conv_state[n].to(dtype))
+        seq = torch.cat([prev, xs[b, start:end].transpose(0, 1)], dim=1)  # [C, W - 1 + len]
+        for t in range(end - start):
+            window = seq[:, t:t + width]  # inputs t - W + 1 .. t
+            y = (window * w).sum(-1)
+            out[b, start + t] = y * torch.sigmoid(y) if activation else y
+        new_state[n] = seq[:, seq.shape[1] - (width - 1):]
+    return out, new_state

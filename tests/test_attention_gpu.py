@@ -1,0 +1,105 @@
+"""Causal grouped-query attention (gdr_attention_fwd) and the segment-aware short convolution (gdr_short_conv_fwd)
+of the hybrid stack, on the GPU, through the package's ops and libgdr.so.
+
+Attention parity uses the reference's own bar (tests/test_flash_attention_2.py:42-53): the kernel's max abs error
+against the exact (fp64) result must be at most 2x that of PyTorch's SDPA run in the same half dtype, plus 1e-4.
+The SDPA baseline runs on the CPU (half-precision attention's math path is kept off this GPU), on the same inputs.
+The short convolution is held to the fp64 oracle at 1e-2 relative to max |out| (one half-precision rounding of
+the output, fp32 accumulation inside).
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _helpers import gdr, oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _qkv(B, H, Hkv, T, D, dtype, seed):
+    gen = torch.Generator().manual_seed(seed)
+    shape_q, shape_kv = (B, H, T, D), (B, Hkv, T, D)
+    return [torch.randn(s, generator=gen).to(dtype) for s in (shape_q, shape_kv, shape_kv)]
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 8, 128, 64), (2, 8, 8, 512, 64), (2, 8, 2, 1000, 128), (3, 12, 4, 777, 64),
+                                   (1, 32, 8, 256, 128), (1, 4, 1, 64, 64), (1, 2, 2, 1, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_attention_matches_exact_within_reference_bar(shape, dtype):
+    B, H, Hkv, T, D = shape
+    print(f"attention {shape} {dtype}", flush=True)
+    q, k, v = _qkv(B, H, Hkv, T, D, dtype, seed=1)
+    exact = oracle.causal_attention(q, k, v)
+    with torch.no_grad():
+        out = gdr.flash_attention(q.cuda(), k.cuda(), v.cuda())
+    sdpa = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)  # CPU, same dtype
+    err = (out.cpu().double() - exact).abs().max().item()
+    base = (sdpa.double() - exact).abs().max().item()
+    print(f"  kernel {err:.2e}  sdpa {base:.2e}")
+    assert out.dtype == dtype and err <= 2 * base + 1e-4
+
+
+def test_attention_packed_sequences_and_layer_layout():
+    """cu_seqlens confines attention to each packed sequence (lengths around the 128-row block and 64-key tile
+    edges, and a single token); q, k, v are the layer's transposed [B, T, H, D] views."""
+    lens = [1, 63, 64, 65, 127, 128, 129, 300]
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    T, H, Hkv, D = int(cu[-1]), 4, 2, 128
+    q, k, v = _qkv(1, H, Hkv, T, D, torch.bfloat16, seed=2)
+    exact = oracle.causal_attention(q, k, v, None, cu)
+    layer = lambda x: x.transpose(1, 2).contiguous().cuda().transpose(1, 2)
+    with torch.no_grad():
+        out = gdr.flash_attention(layer(q), layer(k), layer(v), cu_seqlens=cu.cuda())
+    err = (out.cpu().double() - exact).abs().max().item()
+    print(f"packed: err {err:.2e}")
+    assert err <= 2e-2
+    # every sequence alone gives the same numbers (no leakage across sequence boundaries)
+    with torch.no_grad():
+        for s, e in zip(cu[:-1].tolist(), cu[1:].tolist()):
+            alone = gdr.flash_attention(q[:, :, s:e].cuda(), k[:, :, s:e].cuda(), v[:, :, s:e].cuda())
+            assert torch.equal(alone, out[:, :, s:e].contiguous()), (s, e)
+
+
+def test_attention_scale_and_autocast():
+    q, k, v = _qkv(1, 4, 4, 200, 64, torch.float32, seed=3)
+    exact = oracle.causal_attention(q.bfloat16(), k.bfloat16(), v.bfloat16(), 0.05)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        out = gdr.flash_attention(q.cuda(), k.cuda(), v.cuda(), softmax_scale=0.05)
+    assert out.dtype == torch.bfloat16
+    assert (out.cpu().double() - exact).abs().max().item() <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("width", [2, 4, 8])
+def test_short_convolution_packed_with_state(dtype, width):
+    lens = [1, 2, 5, 64, 100]
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    T, C = int(cu[-1]), 64
+    gen = torch.Generator().manual_seed(4)
+    x = torch.randn(1, T, C, generator=gen).to(dtype)
+    w = (torch.randn(C, 1, width, generator=gen) * 0.5).to(dtype)
+    state = torch.randn(len(lens), C, width - 1, generator=gen).to(dtype)
+    ref, ref_state = oracle.short_convolution(x, w, state, cu)
+    st = state.cuda()
+    with torch.no_grad():
+        out = gdr.short_convolution(x.cuda(), w.cuda(), st, cu_seqlens=cu.cuda())
+    err = ((out.cpu().double() - ref).abs().max() / ref.abs().max()).item()
+    print(f"conv {dtype} W={width}: err {err:.2e}")
+    assert out.dtype == dtype and err <= 1e-2
+    assert torch.equal(st.cpu(), ref_state.to(dtype))  # the new state is a copy of inputs: exact
+
+
+def test_short_convolution_batched_matches_reference_module():
+    """Batched (no cu_seqlens), no state: nn.Conv1d with left padding then SiLU, the reference module's path."""
+    B, T, C, W = 2, 50, 128, 4
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(B, T, C, generator=gen).bfloat16()
+    w = (torch.randn(C, 1, W, generator=gen) * 0.5).bfloat16()
+    ref, _ = oracle.short_convolution(x, w)
+    with torch.no_grad():
+        out = gdr.short_convolution(x.cuda(), w.cuda())
+        plain = gdr.short_convolution(x.cuda(), w.cuda(), activation=False)
+    assert ((out.cpu().double() - ref).abs().max() / ref.abs().max()).item() <= 1e-2
+    lin, _ = oracle.short_convolution(x, w, activation=False)
+    assert ((plain.cpu().double() - lin).abs().max() / lin.abs().max()).item() <= 1e-2

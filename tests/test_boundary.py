@@ -44,6 +44,9 @@ def test_struct_layout_matches_header(tmp_path):
     lines += ['printf("g.size %zu\\n", sizeof(gdr_grads));']
     lines += [f'printf("p.{f} %zu\\n", offsetof(gdr_prologue, {f}));' for f, _ in lib.GdrPrologue._fields_]
     lines += ['printf("p.size %zu\\n", sizeof(gdr_prologue));']
+    for tag, struct, cls in (("a", "gdr_attention_args", lib.GdrAttentionArgs), ("c", "gdr_conv_args", lib.GdrConvArgs)):
+        lines += [f'printf("{tag}.{f} %zu\\n", offsetof({struct}, {f}));' for f, _ in cls._fields_]
+        lines += [f'printf("{tag}.size %zu\\n", sizeof({struct}));']
     lines += ["return 0; }"]
     probe.write_text("\n".join(lines))
     exe = tmp_path / "layout"
@@ -63,6 +66,10 @@ def test_struct_layout_matches_header(tmp_path):
     for f, _ in lib.GdrPrologue._fields_:
         assert int(offsets["p." + f]) == getattr(lib.GdrPrologue, f).offset, f
     assert int(offsets["p.size"]) == ctypes.sizeof(lib.GdrPrologue)
+    for tag, cls in (("a", lib.GdrAttentionArgs), ("c", lib.GdrConvArgs)):
+        for f, _ in cls._fields_:
+            assert int(offsets[f"{tag}.{f}"]) == getattr(cls, f).offset, f
+        assert int(offsets[f"{tag}.size"]) == ctypes.sizeof(cls)
 
 
 def test_last_error_reports_invalid_arguments_without_a_gpu():
@@ -226,3 +233,41 @@ def test_fused_prologue_refuses_gradients_and_cpu_tensors():
     q.requires_grad_()
     with pytest.raises(NotImplementedError, match="no backward"):
         gdr.chunk_kimi_delta_attention_fused(q, k, v, z, w, None, a_log, b)
+
+
+def test_attention_and_conv_reject_bad_arguments_without_a_gpu():
+    so = lib.load_library()
+    a = lib.GdrAttentionArgs()
+    a.abi_version = lib.ABI_VERSION
+    a.batch, a.heads, a.kv_heads, a.seq_len, a.head_dim = 1, 6, 4, 16, 64
+    assert so.gdr_attention_fwd(ctypes.byref(a), None) == -1
+    assert b"does not divide" in so.gdr_last_error()
+    a.kv_heads, a.head_dim = 2, 96
+    assert so.gdr_attention_fwd(ctypes.byref(a), None) == -2
+    assert b"head dim 96" in so.gdr_last_error()
+    a.head_dim = 64
+    for name, off in (("q", 256), ("k", 512), ("v", 768), ("out", 1024)):
+        view = getattr(a, name)
+        view.ptr, view.dtype = off, lib.F32
+    assert so.gdr_attention_fwd(ctypes.byref(a), None) == -2
+    assert b"bf16 or f16" in so.gdr_last_error()
+    c = lib.GdrConvArgs()
+    c.abi_version = lib.ABI_VERSION
+    c.batch, c.seq_len, c.channels, c.kernel_size = 1, 8, 64, 9
+    assert so.gdr_short_conv_fwd(ctypes.byref(c), None) == -2
+    assert b"kernel size 9" in so.gdr_last_error()
+    c.kernel_size = 4
+    c.x.ptr, c.x.dtype, c.out.ptr, c.out.dtype = 256, lib.BF16, 512, lib.BF16
+    c.weight, c.state_in, c.state_out = 1024, 2048, 2048
+    assert so.gdr_short_conv_fwd(ctypes.byref(c), None) == -1
+    assert b"alias" in so.gdr_last_error()
+
+
+def test_stack_ops_refuse_cpu_tensors_and_gradients():
+    q = torch.randn(1, 2, 8, 64)
+    with pytest.raises(ValueError, match="GPU"):
+        gdr.flash_attention(q, q, q)
+    with pytest.raises(NotImplementedError, match="forward only"):
+        gdr.flash_attention(q.requires_grad_(), q, q)
+    with pytest.raises(ValueError, match="GPU"):
+        gdr.short_convolution(torch.randn(1, 8, 64), torch.randn(64, 1, 4))

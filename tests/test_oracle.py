@@ -235,3 +235,47 @@ def test_layer_prologue_matches_torch_functional():
     torch.testing.assert_close(kn, F.normalize(k, dim=-1), rtol=1e-12, atol=1e-12)
     torch.testing.assert_close(beta, torch.sigmoid(logits), rtol=1e-12, atol=1e-12)
     assert torch.count_nonzero(qn[0, 0, 0]) == 0
+
+
+def test_causal_attention_matches_sdpa_and_is_per_sequence():
+    gen = torch.Generator().manual_seed(6)
+    q = torch.randn(2, 6, 37, 16, generator=gen, dtype=torch.float64)
+    k = torch.randn(2, 2, 37, 16, generator=gen, dtype=torch.float64)
+    v = torch.randn(2, 2, 37, 16, generator=gen, dtype=torch.float64)
+    ref = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True, scale=0.3)
+    torch.testing.assert_close(oracle.causal_attention(q, k, v, 0.3), ref, rtol=1e-12, atol=1e-12)
+    cu = torch.tensor([0, 1, 12, 37])
+    packed = oracle.causal_attention(q[:1], k[:1], v[:1], None, cu)
+    for s, e in zip(cu[:-1].tolist(), cu[1:].tolist()):
+        alone = oracle.causal_attention(q[:1, :, s:e], k[:1, :, s:e], v[:1, :, s:e])
+        torch.testing.assert_close(packed[:, :, s:e], alone, rtol=0, atol=0)
+
+
+def test_short_convolution_matches_conv1d_and_state_path():
+    """Against the reference module's own computations: nn.Conv1d with left padding (no state) and F.conv1d over
+    [state, x] with the state replaced by the last W - 1 inputs (src/layers/short_convolution.py:13-19)."""
+    gen = torch.Generator().manual_seed(7)
+    B, T, C, W = 2, 9, 6, 4
+    x = torch.randn(B, T, C, generator=gen, dtype=torch.float64)
+    conv = torch.nn.Conv1d(C, C, W, groups=C, padding=W - 1, bias=False).double()
+    with torch.no_grad():
+        conv.weight.copy_(torch.randn(C, 1, W, generator=gen, dtype=torch.float64))
+        ref = F.silu(conv(x.transpose(1, 2))[..., :T]).transpose(1, 2)
+    out, state = oracle.short_convolution(x, conv.weight.detach())
+    torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(state, x[:, T - (W - 1):].transpose(1, 2), rtol=0, atol=0)
+    prev = torch.randn(B, C, W - 1, generator=gen, dtype=torch.float64)
+    seq = torch.cat([prev, x.transpose(1, 2)], dim=-1)
+    ref2 = F.silu(F.conv1d(seq, conv.weight.detach(), groups=C)).transpose(1, 2)
+    out2, state2 = oracle.short_convolution(x, conv.weight.detach(), prev)
+    torch.testing.assert_close(out2, ref2, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(state2, seq[..., -(W - 1):], rtol=0, atol=0)
+    # packed: each sequence restarts from its own state, including one shorter than W - 1
+    cu = torch.tensor([0, 2, 9])
+    xp = x[:1]
+    outp, statep = oracle.short_convolution(xp, conv.weight.detach(), prev, cu)
+    for n, (s, e) in enumerate(zip(cu[:-1].tolist(), cu[1:].tolist())):
+        alone, st = oracle.short_convolution(xp[:, s:e], conv.weight.detach(), prev[n:n + 1])
+        torch.testing.assert_close(outp[:, s:e], alone, rtol=0, atol=0)
+        torch.testing.assert_close(statep[n], st[0], rtol=0, atol=0)
+    assert torch.equal(statep[0, :, :1], prev[0, :, 2:]) and torch.equal(statep[0, :, 1:], xp[0, :2].t())
