@@ -18,6 +18,9 @@ One JSON line on stdout:
   * fused: the prefill configuration from the KDA layer's pre-op tensors (q, k before normalisation, beta logits,
     the gate's rank-128 activations with decay_proj[1]'s weight and bias), as one gdr_chunk_fwd_fused call, beside
     the same preparation done in PyTorch followed by the plain op (what the reference layer runs).
+  * stack: the packed-prefill configuration through the hybrid stack harness (3 KDA blocks and 1 attention block
+    of the 0.6B model's shapes, random bf16 weights, 32 sequences with lengths ~U[256, 4096]): end-to-end tokens/s
+    and the KDA op's share of the time.
   * train: the prefill configuration under torch.autograd, forward then backward (gdr_chunk_bwd), with the
     backward's algorithmic bytes and HBM fraction.
   * cpu_baseline: the reference's CPU path for the op (fp32 token loop, restated in oracle/) timed on this
@@ -295,6 +298,37 @@ def bench_varlen(gdr, workloads, torch, steps, warmup):
             "note": "KDA op only (the layer stack around it is out of scope)"}
 
 
+def bench_stack(gdr, workloads, torch, steps, warmup):
+    stack = importlib.import_module("gtar-kimik3-public_amd.stack")
+    cfg = stack.StackConfig()
+    model = stack.HybridStack(cfg, stack.init_weights(cfg, seed=0))
+    lengths = workloads.varlen_lengths(VARLEN["n_seqs"], VARLEN["low"], VARLEN["high"], seed=0)
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0).tolist()), dtype=torch.int32, device="cuda")
+    tokens = int(cu[-1])
+    hidden = torch.randn(1, tokens, cfg.hidden_size, generator=torch.Generator().manual_seed(1)).bfloat16().cuda()
+    for _ in range(warmup):
+        model.forward(hidden, cu)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    total, kda = 0.0, 0.0
+    for _ in range(steps):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        model.forward(hidden, cu, timed=True)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        total += start.elapsed_time(stop)
+        kda += sum(a.elapsed_time(b) for a, b in model.kda_op_events)
+    total, kda = total / steps, kda / steps
+    return {"workload": "hybrid_stack_packed_prefill", "n_seqs": len(lengths), "tokens": tokens,
+            "layers": f"{cfg.num_layers} ({cfg.num_layers - cfg.num_layers // cfg.attention_interval} KDA, "
+                      f"{cfg.num_layers // cfg.attention_interval} attention)",
+            "hidden": cfg.hidden_size, "ms_per_forward": round(total, 3), "tokens_per_s": round(tokens / (total * 1e-3), 1),
+            "kda_op_ms": round(kda, 3), "kda_op_share": round(kda / total, 4),
+            "note": "random bf16 weights; projections, norms and MLP in PyTorch; KDA, attention and short convolution "
+                    "on this package's kernels"}
+
+
 def train_bytes(B, T, H, K, V, **_):
     """Algorithmic HBM bytes of one chunk backward: read q, k, v (bf16), gate (fp32), beta, dO (bf16), h0 and the
     final-state gradient; write dq, dk, dv (bf16), dgate, dbeta (fp32) and dh0."""
@@ -377,6 +411,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-verify", action="store_true", help="skip the speculative verify + commit leg")
     ap.add_argument("--no-fused", action="store_true", help="skip the fused-prologue prefill leg")
+    ap.add_argument("--no-stack", action="store_true", help="skip the hybrid stack harness leg")
     ap.add_argument("--no-varlen", action="store_true", help="skip the packed varlen prefill leg")
     ap.add_argument("--no-train", action="store_true", help="skip the forward + backward (autograd) leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="minimum seconds of CPU baseline work")
@@ -433,6 +468,8 @@ def main():
         record["fused"] = bench_fused(gdr, torch, steps=20, warmup=5)
     if not opts.no_varlen:
         record["varlen"] = bench_varlen(gdr, workloads, torch, steps=10, warmup=3)
+    if not opts.no_stack:
+        record["stack"] = bench_stack(gdr, workloads, torch, steps=5, warmup=2)
     if not opts.no_train:
         record["train"] = bench_train(gdr, workloads, torch, steps=5, warmup=2)
     if opts.copy_mib:

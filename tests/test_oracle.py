@@ -279,3 +279,10 @@ def test_short_convolution_matches_conv1d_and_state_path():
         torch.testing.assert_close(outp[:, s:e], alone, rtol=0, atol=0)
         torch.testing.assert_close(statep[n], st[0], rtol=0, atol=0)
     assert torch.equal(statep[0, :, :1], prev[0, :, 2:]) and torch.equal(statep[0, :, 1:], xp[0, :2].t())
+
+
+def test_rms_norm_matches_functional():
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn(5, 7, 16, generator=gen, dtype=torch.float64)
+    w = torch.randn(16, generator=gen, dtype=torch.float64)
+    torch.testing.assert_close(oracle.rms_norm(x, w, 1e-6), F.rms_norm(x, (16,), w, 1e-6), rtol=1e-12, atol=1e-12)
