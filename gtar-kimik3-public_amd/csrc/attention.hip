@@ -21,6 +21,7 @@ namespace gdr {
 namespace {
 
 using chunk::kLog2e;
+using chunk::lds_dma16;
 using chunk::lds_read_tr;
 using chunk::pack4;
 
@@ -59,12 +60,6 @@ struct Mma<_Float16> {
 template <typename V4, typename V8>
 __device__ __forceinline__ V8 cat(V4 lo, V4 hi) {
   return V8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
-// 16 bytes from global memory straight into LDS (global_load_lds_dwordx4): lane i's bytes land at the wave-uniform
-// LDS address `lds_base` + 16 i.
-__device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
 
 // First query-block slot of packed sequence n: floor(bos / kBM) + n (slots of consecutive sequences never overlap).

@@ -44,6 +44,12 @@ __device__ __forceinline__ bf16x4 lds_read_tr(const unsigned char* smem, int byt
   return __builtin_bit_cast(bf16x4, v);
 }
 
+// 16 bytes from global memory straight into LDS (global_load_lds_dwordx4): lane i's bytes land at the wave-uniform
+// LDS address `lds_base` + 16 i.
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
 // Workgroup barrier that orders LDS only: global stores issued before it are not waited for (a full
 // __syncthreads() also drains outstanding global memory operations).
 __device__ __forceinline__ void lds_barrier() {

@@ -50,6 +50,11 @@ CASES = [
     (1, 2, 1, 128, 128, 1.0, 0.02),
     (1, 3, 65, 128, 128, 1.0, 0.02),
     (3, 2, 130, 128, 192, 1.0, 0.02),
+    # eight and sixteen heads (the prefill configuration's head count), short and ragged
+    (1, 8, 200, 128, 128, 16.0, 1.0),
+    (2, 8, 513, 128, 128, 1.0, 0.02),
+    (1, 8, 1, 128, 128, 1.0, None),
+    (1, 16, 64, 128, 128, 0.1, 1.0),
 ]
 
 
@@ -135,6 +140,39 @@ def test_chunk_prefill_config_full_size():
     print("chunk kda B=4 T=4096 H=16 K=V=128", flush=True)
     inp = workloads.make_inputs("kda", 4, 4096, 16, 128, 128, seed=0, state_std=0.02, device="cuda")
     _check("kda", inp, "chunk kda full size")
+
+
+def test_chunk_back_to_back_calls_reuse_workspace():
+    """Calls enqueued back to back without synchronisation, each reusing the memory of the previous call's workspace
+    (the earlier call's records are still in it), give the same results as calls run one at a time."""
+    a = workloads.make_inputs("kda", 2, 700, 8, 128, 128, seed=11, state_std=0.02, device="cuda")
+    b = workloads.make_inputs("kda", 2, 700, 8, 128, 128, seed=12, state_std=0.02, device="cuda")
+    runs = [_run("kda", x) for x in (a, b, a, b)]
+    torch.cuda.synchronize()
+    assert torch.equal(runs[0][0], runs[2][0]) and torch.equal(runs[0][1], runs[2][1])
+    assert torch.equal(runs[1][0], runs[3][0]) and torch.equal(runs[1][1], runs[3][1])
+    _check("kda", b, "chunk kda second input")
+
+
+def test_chunk_under_graph_capture_matches_eager():
+    """A captured prefill replays to the eager result, with eager work and synchronisation between the replays."""
+    inp = workloads.make_inputs("kda", 1, 300, 8, 128, 128, seed=13, state_std=0.02, device="cuda")
+    eager_o, eager_s = _run("kda", inp)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _run("kda", inp)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap_o, cap_s = _run("kda", inp)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(cap_o, eager_o) and torch.equal(cap_s, eager_s)
+        _run("kda", inp)  # eager work between replays
+        torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("variant", ["gdn", "gla", "deltanet"])
