@@ -136,8 +136,8 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
 
   // ---- workgroup -> (sequence n, head h, chunk c) ----
   const int H = a.heads;
-  const int h = blockIdx.x % H, slot = blockIdx.x / H;
-  int n, c, bos = 0, len = a.seq_len;
+  const int h = blockIdx.x % H;
+  int slot = blockIdx.x / H, n, c, bos = 0, len = a.seq_len;
   if (a.cu_seqlens) {
     int lo = 0, hi = a.n_seqs - 1;  // largest n with base(n) <= slot
     while (lo < hi) {
@@ -150,8 +150,11 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
     c = slot - varlen_base(a.cu_seqlens, n);
     if (c < 0 || c * kChunk >= len) return;  // gap slot: uniform over the workgroup, before any barrier
   } else {
-    n = slot / nc;
-    c = slot % nc;
+    // Launch order is chunk-major from the last chunk down: the records written last are the first chunks, which
+    // the scan reads first, so they are the ones still held by the memory-side cache when it starts.
+    n = slot % a.batch;
+    c = nc - 1 - slot / a.batch;
+    slot = n * nc + c;
   }
   const int bidx = a.cu_seqlens ? 0 : n;
   ChunkCtx x;
