@@ -12,6 +12,7 @@ and `short_convolution` (src/layers/short_convolution.py) take packed sequences 
 from .attention import flash_attention
 from .cache import RecurrentCache
 from .conv import short_convolution
+from .epilogue import output_norm_gate
 from .deltanet import chunk_deltanet, recurrent_deltanet, verify_deltanet
 from .fused import chunk_gated_linear_attention_fused, chunk_kimi_delta_attention_fused
 from .gated_deltanet import chunk_gated_deltanet, recurrent_gated_deltanet, verify_gated_deltanet
@@ -29,6 +30,7 @@ __all__ = [
     "chunk_kimi_delta_attention",
     "chunk_kimi_delta_attention_fused",
     "flash_attention",
+    "output_norm_gate",
     "recurrent_deltanet",
     "recurrent_gated_deltanet",
     "recurrent_gated_linear_attention",

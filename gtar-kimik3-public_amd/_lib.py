@@ -18,8 +18,8 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.join(_HERE, "libgdr.so")
-ABI_VERSION = 6
-PRO_NORM_QK, PRO_BETA_LOGITS, PRO_GATE_LOWRANK = 1, 2, 4
+ABI_VERSION = 7
+PRO_NORM_QK, PRO_BETA_LOGITS, PRO_GATE_LOWRANK, PRO_CONV = 1, 2, 4, 8
 
 KDA, GDN, GLA, DELTANET = 0, 1, 2, 3
 F32, BF16, F16 = 0, 1, 2
@@ -71,6 +71,11 @@ class GdrPrologue(ctypes.Structure):
         ("gate_weight", ctypes.c_void_p),
         ("gate_bias", ctypes.c_void_p),
         ("a_log", ctypes.c_void_p),
+        ("conv_size", ctypes.c_int32),
+        ("conv_reserved", ctypes.c_int32),
+        ("conv_weight", ctypes.c_void_p * 3),
+        ("conv_state_in", ctypes.c_void_p * 3),
+        ("conv_state_out", ctypes.c_void_p * 3),
     ]
 
 
@@ -111,6 +116,23 @@ class GdrConvArgs(ctypes.Structure):
     ]
 
 
+class GdrNormGateArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("seq_len", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("value_dim", ctypes.c_int32),
+        ("weight_dtype", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+        ("x", GdrTensor),
+        ("gate", GdrTensor),
+        ("out", GdrTensor),
+        ("weight", ctypes.c_void_p),
+    ]
+
+
 class GdrGrads(ctypes.Structure):
     _fields_ = [
         ("d_out", GdrTensor),
@@ -138,6 +160,7 @@ EXPORTS = {
                                             ctypes.c_void_p]),
     "gdr_attention_fwd": (ctypes.c_int, [ctypes.POINTER(GdrAttentionArgs), ctypes.c_void_p]),
     "gdr_short_conv_fwd": (ctypes.c_int, [ctypes.POINTER(GdrConvArgs), ctypes.c_void_p]),
+    "gdr_norm_gate_fwd": (ctypes.c_int, [ctypes.POINTER(GdrNormGateArgs), ctypes.c_void_p]),
     "gdr_last_error": (ctypes.c_char_p, []),
     "gdr_abi_version": (ctypes.c_int, []),
 }
@@ -274,9 +297,16 @@ def commit(args: GdrArgs, updates: torch.Tensor, accepted: torch.Tensor | None, 
                                                             acc, ctypes.c_void_p(stream)))
 
 
-def make_prologue(flags: int, gate_lowrank=None, gate_weight=None, gate_bias=None, a_log=None) -> GdrPrologue:
+def make_prologue(flags: int, gate_lowrank=None, gate_weight=None, gate_bias=None, a_log=None, conv_weights=None,
+                  conv_states_in=None, conv_states_out=None) -> GdrPrologue:
     pro = GdrPrologue()
     pro.flags = flags
+    if conv_weights is not None:
+        pro.conv_size = conv_weights[0].shape[-1]
+        for i in range(3):
+            pro.conv_weight[i] = conv_weights[i].data_ptr()
+            pro.conv_state_in[i] = conv_states_in[i].data_ptr() if conv_states_in is not None else None
+            pro.conv_state_out[i] = conv_states_out[i].data_ptr() if conv_states_out is not None else None
     if gate_lowrank is not None:
         pro.rank = gate_lowrank.shape[-1]
         view = GdrTensor()
@@ -340,3 +370,28 @@ def short_conv(x, out, weight, state_in, state_out, cu_seqlens, silu, device) ->
     lib = load_library()
     stream = torch.cuda.current_stream(device).cuda_stream
     _check("gdr_short_conv_fwd", lib.gdr_short_conv_fwd(ctypes.byref(args), ctypes.c_void_p(stream)))
+
+
+def norm_gate(x, gate, weight, out, eps, device) -> None:
+    """Enqueue gdr_norm_gate_fwd on torch's current stream; x, gate, out are [B, T, H, V] views."""
+    args = GdrNormGateArgs()
+    args.abi_version = ABI_VERSION
+    args.batch, args.seq_len, args.heads, args.value_dim = x.shape
+    args.weight_dtype = _DTYPE_CODES[weight.dtype]
+    args.eps = float(eps)
+
+    def bthv(t, name):
+        if t.dtype not in _DTYPE_CODES:
+            raise TypeError(f"{name}: unsupported dtype {t.dtype}")
+        if t.shape[-1] > 1 and t.stride(-1) != 1:
+            raise ValueError(f"{name}: the last dimension must be contiguous")
+        view = GdrTensor()
+        view.ptr, view.dtype = t.data_ptr(), _DTYPE_CODES[t.dtype]
+        view.stride_b, view.stride_h, view.stride_t = t.stride(0), t.stride(2), t.stride(1)
+        return view
+
+    args.x, args.gate, args.out = bthv(x, "x"), bthv(gate, "gate"), bthv(out, "out")
+    args.weight = weight.data_ptr()
+    lib = load_library()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    _check("gdr_norm_gate_fwd", lib.gdr_norm_gate_fwd(ctypes.byref(args), ctypes.c_void_p(stream)))

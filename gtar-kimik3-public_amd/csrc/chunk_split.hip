@@ -70,6 +70,67 @@ __device__ __forceinline__ float softplus_f32(float x) {
   return fmaxf(x, 0.f) + l1p;
 }
 
+// The fused prologue's short convolution (ShortConvolution, src/layers/short_convolution.py:11-20; width 4):
+// silu(sum_{j < 4} w[c][j] x[t - 3 + j][c]) for 8 consecutive channels at the 4 sequence rows r0 .. r0 + 3, accumulated
+// in fp32 and rounded once to bf16 (as gdr_short_conv_fwd).  The 7 input rows r0 - 3 .. r0 + 3 are loaded once;
+// rows before the sequence come from its conv state [C][3] (`st8` points at the first of the 8 channels' rows) or are
+// zero, and rows past `last` (the sequence's last row) read row `last` (their outputs are masked by the caller).
+// `x0` is row 0 of the sequence at the first channel, `w8` the 8 channels' weight rows ([8][4], 64 contiguous bytes).
+__device__ __forceinline__ void conv4_silu8x4(const __bf16* x0, int64_t x_st, int r0, int last, const __bf16* w8,
+                                              const __bf16* st8, uint4 (&out)[4]) {
+  uint32_t w[16];  // packed bf16 pairs: weight (e, j) is bf16 number 4 e + j
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint4 wu = *reinterpret_cast<const uint4*>(w8 + 8 * u);
+    w[4 * u] = wu.x, w[4 * u + 1] = wu.y, w[4 * u + 2] = wu.z, w[4 * u + 3] = wu.w;
+  }
+  auto wf = [&](int m) {  // bf16 number m as fp32
+    const uint32_t word = w[m >> 1];
+    return __uint_as_float((m & 1) ? (word & 0xffff0000u) : (word << 16));
+  };
+  uint4 xr[7];
+#pragma unroll
+  for (int m = 0; m < 7; ++m) {
+    const int r = r0 - 3 + m;
+    if (r >= 0) {
+      xr[m] = *reinterpret_cast<const uint4*>(x0 + int64_t(min(r, last)) * x_st);
+    } else {
+      bf16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = st8 ? st8[3 * e + 3 + r] : bf(0.f);
+      xr[m] = __builtin_bit_cast(uint4, v);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float xv[8];
+      unpack8(xr[i + j], xv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += wf(4 * e + j) * xv[e];
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = bf(acc[e] / (1.f + __builtin_amdgcn_exp2f(-acc[e] * kLog2e)));
+    out[i] = __builtin_bit_cast(uint4, o);
+  }
+}
+
+// The same for one channel (the hot-channel re-fetch), returned as the bf16-rounded value.
+__device__ __forceinline__ float conv4_silu1(const __bf16* x0, int64_t x_st, int t, const __bf16* w4,
+                                            const __bf16* st3) {
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = t - 3 + j;
+    const float xv = r >= 0 ? f32(x0[int64_t(r) * x_st]) : (st3 ? f32(st3[3 + r]) : 0.f);
+    acc += f32(w4[j]) * xv;
+  }
+  return f32(bf(acc / (1.f + __builtin_amdgcn_exp2f(-acc * kLog2e))));
+}
+
 // The low-rank gate of the fused prologue for the chunk's 64 rows:
 //   g[t][c] = -e^{A_log[h]} softplus(z_t . W[h K + c] + bias[h K + c])
 // Wave w computes channels [w K / 4, (w + 1) K / 4) of all 64 rows as Gᵀ = W_h Zᵀ on v_mfma_f32_16x16x32_bf16 (A = 16
@@ -119,11 +180,13 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
 
 // ======================================= prep: one workgroup per (chunk, head) =======================================
 // kPro: the fused layer prologue.  0: none (the plain op); 1: `pro.flags` selects the in-kernel q / k
-// normalisation and the beta sigmoid; 2: as 1, and the per-channel gate comes from the low-rank projection.
+// normalisation and the beta sigmoid; 2: as 1, and the per-channel gate comes from the low-rank projection; plus 4:
+// the short convolutions of q, k, v run in the kernel too.
 template <int VARIANT, int K, int kPro = 0>
 __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr_args a, int nc, int64_t rec_bytes,
                                                                        const gdr_prologue pro) {
-  constexpr bool kLowRank = kPro == 2;
+  constexpr bool kLowRank = (kPro & 3) == 2;
+  constexpr bool kConv = (kPro & 4) != 0;
   static_assert(!kLowRank || VARIANT == GDR_KDA || VARIANT == GDR_GLA, "low-rank gate: per-channel variants");
   constexpr bool kDelta = VARIANT != GDR_GLA;
   constexpr int kGate = (VARIANT == GDR_KDA || VARIANT == GDR_GLA) ? 2 : (VARIANT == GDR_GDN ? 1 : 0);
@@ -172,6 +235,16 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
   x.len = len;
   x.nchunks = 0; x.v0 = 0; x.V = a.value_dim; x.sbase = 0; x.h0 = nullptr; x.ht = nullptr; x.scale = 0.f;
   unsigned char* rec = static_cast<unsigned char*>(a.workspace) + (int64_t(slot) * H + h) * rec_bytes;
+  // fused prologue: in-kernel short convolutions of q, k, v (channels h K + ch of [H K] for q, k; h V + col for v)
+  constexpr bool conv = kConv;
+  const int64_t ck = int64_t(H) * K, cv = int64_t(H) * a.value_dim;
+  const __bf16* cwq = static_cast<const __bf16*>(pro.conv_weight[0]) + (int64_t(h) * K) * 4;
+  const __bf16* cwk = static_cast<const __bf16*>(pro.conv_weight[1]) + (int64_t(h) * K) * 4;
+  const __bf16* cwv = static_cast<const __bf16*>(pro.conv_weight[2]) + (int64_t(h) * a.value_dim) * 4;
+  auto state_rows = [&](int i, int64_t nch, int64_t ch0) -> const __bf16* {  // [C][3] rows of this sequence
+    const __bf16* st = static_cast<const __bf16*>(pro.conv_state_in[i]);
+    return st ? st + (int64_t(n) * nch + ch0) * 3 : nullptr;
+  };
 
   __bf16* kap = reinterpret_cast<__bf16*>(smem + L::KAP);
   __bf16* vst = reinterpret_cast<__bf16*>(smem + L::VST);
@@ -200,24 +273,37 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
   constexpr int kVLoads = (kVPieces + 255) / 256;      // per thread
   const int n_pass = (a.value_dim + K - 1) / K;
   auto pass_width = [&](int pass) { return min(K, a.value_dim - pass * K); };
-  uint4 vpre[kVLoads];
+  // With the in-kernel convolution, thread u (< 16 w8) holds rows 4 (u / w8) .. + 3 of column group u % w8 (the four
+  // rows share their input window); otherwise piece i of a thread is 16-byte piece threadIdx.x + 256 i of the pass.
+  constexpr int kVRegs = kConv ? 4 : kVLoads;
+  static_assert(!kConv || 16 * K / 8 <= 256, "conv mapping: one row quad per thread");
+  uint4 vpre[kVRegs];
   auto load_v_pass = [&](int pass) {  // unconditional loads from clamped rows / pieces; masked when staged
     const int w8 = pass_width(pass) / 8;
+    if constexpr (kConv) {
+      const int u = min(int(threadIdx.x), 16 * w8 - 1);
+      const int col = pass * K + (u % w8) * 8;
+      conv4_silu8x4(x.vp + col, x.v_st, c * kChunk + 4 * (u / w8), len - 1, cwv + col * 4,
+                    state_rows(2, cv, int64_t(h) * a.value_dim + col), vpre);
+    } else {
 #pragma unroll
-    for (int i = 0; i < kVLoads; ++i) {
-      const int pc = min(int(threadIdx.x) + 256 * i, 64 * w8 - 1);
-      const int row = pc / w8, cc = (pc % w8) * 8;
-      const int t = min(c * kChunk + row, len - 1);
-      vpre[i] = *reinterpret_cast<const uint4*>(x.vp + t * x.v_st + pass * K + cc);
+      for (int i = 0; i < kVLoads; ++i) {
+        const int pc = min(int(threadIdx.x) + 256 * i, 64 * w8 - 1);
+        const int row = pc / w8, cc = (pc % w8) * 8;
+        const int t = min(c * kChunk + row, len - 1);
+        vpre[i] = *reinterpret_cast<const uint4*>(x.vp + t * x.v_st + pass * K + cc);
+      }
     }
   };
   auto stage_v_pass = [&](int pass) {
     const int w8 = pass_width(pass) / 8;
 #pragma unroll
-    for (int i = 0; i < kVLoads; ++i) {
+    for (int i = 0; i < kVRegs; ++i) {
       const int pc = threadIdx.x + 256 * i;
-      if (pc < 64 * w8) {
-        const int row = pc / w8, cc = (pc % w8) * 8;
+      const int u = threadIdx.x;
+      const bool have = kConv ? u < 16 * w8 : pc < 64 * w8;
+      if (have) {
+        const int row = kConv ? 4 * (u / w8) + i : pc / w8, cc = kConv ? (u % w8) * 8 : (pc % w8) * 8;
         const uint32_t keep = c * kChunk + row < len ? 0xffffffffu : 0u;
         *reinterpret_cast<uint4*>(vst + row * KP + cc) =
             make_uint4(vpre[i].x & keep, vpre[i].y & keep, vpre[i].z & keep, vpre[i].w & keep);
@@ -236,12 +322,50 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
                          reinterpret_cast<float*>(smem), wave, l16, g4);
     __syncthreads();
   }
+  if constexpr (kConv) {
+    // The convolved q, k rows are staged in the KAP / KD tiles (bf16 [64][KP]; free until step 3b): unit u covers
+    // rows 4 (u / (K / 8)) .. + 3 of channel group u % (K / 8) of tensor u / (16 K / 8).  Low-rank gate rows, which
+    // occupy the same region, are read first.
+    if constexpr (kLowRank) {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const float* gr = reinterpret_cast<const float*>(smem) + (16 * p + l16) * (K + 4) + 32 * kk + 8 * g4;
+        const float4 g0 = *reinterpret_cast<const float4*>(gr);
+        const float4 g1 = *reinterpret_cast<const float4*>(gr + 4);
+        bl[kk][0] = g0.x; bl[kk][1] = g0.y; bl[kk][2] = g0.z; bl[kk][3] = g0.w;
+        bl[kk][4] = g1.x; bl[kk][5] = g1.y; bl[kk][6] = g1.z; bl[kk][7] = g1.w;
+      }
+      __syncthreads();
+    }
+    constexpr int G8 = K / 8, kUnits = 2 * 16 * G8;
+#pragma unroll
+    for (int u0 = 0; u0 < kUnits; u0 += 256) {
+      const int u = u0 + threadIdx.x;
+      if (u < kUnits) {
+        const int tsr = u / (16 * G8), rq = (u / G8) % 16, ch = (u % G8) * 8;
+        uint4 o[4];
+        conv4_silu8x4((tsr ? x.kp : x.qp) + ch, tsr ? x.k_st : x.q_st, c * kChunk + 4 * rq, len - 1,
+                      (tsr ? cwk : cwq) + ch * 4, state_rows(tsr, ck, int64_t(h) * K + ch), o);
+        __bf16* tile = tsr ? kd : kap;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(tile + (4 * rq + i) * KP + ch) = o[i];
+      }
+    }
+    __syncthreads();
+  }
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {
     const int ch = 32 * kk + 8 * g4;
-    qraw[kk] = *reinterpret_cast<const uint4*>(x.qp + tc * x.q_st + ch);
-    kraw[kk] = *reinterpret_cast<const uint4*>(x.kp + tc * x.k_st + ch);
-    if constexpr (kLowRank) {
+    if constexpr (kConv) {
+      qraw[kk] = *reinterpret_cast<const uint4*>(kap + (16 * p + l16) * KP + ch);
+      kraw[kk] = *reinterpret_cast<const uint4*>(kd + (16 * p + l16) * KP + ch);
+    } else {
+      qraw[kk] = *reinterpret_cast<const uint4*>(x.qp + tc * x.q_st + ch);
+      kraw[kk] = *reinterpret_cast<const uint4*>(x.kp + tc * x.k_st + ch);
+    }
+    if constexpr (kLowRank && kConv) {
+      // bl was read before the conv stage
+    } else if constexpr (kLowRank) {
       const float* gr = reinterpret_cast<const float*>(smem) + (16 * p + l16) * (K + 4) + ch;
       const float4 g0 = *reinterpret_cast<const float4*>(gr);
       const float4 g1 = *reinterpret_cast<const float4*>(gr + 4);
@@ -449,13 +573,17 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
         hot_diag_fixup<K, kDelta>(c * kChunk, p, len, hot_mask, sct + tri_tile(p, p) * 256, lii + p * 256,
                                   sbeta + 16 * p, rows);
       };
-      if (kPro && (kLowRank || (pro.flags & GDR_PRO_NORM_QK))) {
+      if (kPro && (kLowRank || kConv || (pro.flags & GDR_PRO_NORM_QK))) {
         // The fused prologue's inputs are not in memory as the kernel used them: q, k are renormalised with the
         // row norms kept in LDS, and the gate is recomputed from z and W (the R-long dot split over the 4 lanes
         // that share a row).
         const bool norm = pro.flags & GDR_PRO_NORM_QK;
         auto rows = [&](int tcr, int ch, float& q, float& k, float& g) {
           InputRows{x, kGate}(tcr, ch, q, k, g);  // g is replaced below when it is computed
+          if (conv) {
+            q = conv4_silu1(x.qp + ch, x.q_st, tcr, cwq + ch * 4, state_rows(0, ck, int64_t(h) * K + ch));
+            k = conv4_silu1(x.kp + ch, x.k_st, tcr, cwk + ch * 4, state_rows(1, ck, int64_t(h) * K + ch));
+          }
           const int r = tcr - c * kChunk;          // row within the chunk (clamped rows stay inside it)
           if (norm) q = f32(bf(q * snorm[r])), k = f32(bf(k * snorm[64 + r]));
           if constexpr (kLowRank) {
@@ -573,6 +701,31 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
     }
     const int tiles = pass_width(pass) / 16;
     for (int nt = wave; nt < tiles; nt += 4) solve_tile(L::VST, 16 * nt, false, pass * K + 16 * nt);
+  }
+
+  // fused prologue: the last chunk of a sequence stores the last 3 inputs of each of its head's q, k, v channels,
+  // reaching back into the state it was given when the sequence is shorter than 3
+  if (conv && (c + 1) * kChunk >= len) {
+    const int V = a.value_dim, nqk = 2 * K * 3, ntot = nqk + V * 3;
+    for (int idx = threadIdx.x; idx < ntot; idx += 256) {
+      const int i = idx < nqk ? idx / (K * 3) : 2;
+      const int rem = idx < nqk ? idx % (K * 3) : idx - nqk, ch = rem / 3, sl = rem % 3;
+      __bf16* so = static_cast<__bf16*>(pro.conv_state_out[i]);
+      if (!so) continue;
+      const int64_t nch = i < 2 ? ck : cv;
+      const int64_t row = int64_t(n) * nch + (i < 2 ? int64_t(h) * K : int64_t(h) * V) + ch;
+      const int r = len - 3 + sl;
+      __bf16 val;
+      if (r >= 0) {
+        const __bf16* xp = i == 0 ? x.qp : i == 1 ? x.kp : x.vp;
+        const int64_t xs = i == 0 ? x.q_st : i == 1 ? x.k_st : x.v_st;
+        val = xp[int64_t(r) * xs + ch];
+      } else {
+        const __bf16* si = static_cast<const __bf16*>(pro.conv_state_in[i]);
+        val = si ? si[row * 3 + sl + len] : bf(0.f);
+      }
+      so[row * 3 + sl] = val;
+    }
   }
 }
 
@@ -844,13 +997,16 @@ hipError_t launch_split_typed(const gdr_args& a, const gdr_prologue& pro, hipStr
   const int64_t rec = Rec<K>::bytes(a.value_dim);
   constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::UT_SLICE);
   hipError_t e;
+  const bool conv = pro.flags & GDR_PRO_CONV;
   if (!pro.flags) {
     e = launch_prep<VARIANT, K, 0>(a, pro, stream);
   } else if constexpr (VARIANT == GDR_KDA || VARIANT == GDR_GLA) {
-    e = (pro.flags & GDR_PRO_GATE_LOWRANK) ? launch_prep<VARIANT, K, 2>(a, pro, stream)
-                                           : launch_prep<VARIANT, K, 1>(a, pro, stream);
+    if (pro.flags & GDR_PRO_GATE_LOWRANK)
+      e = conv ? launch_prep<VARIANT, K, 6>(a, pro, stream) : launch_prep<VARIANT, K, 2>(a, pro, stream);
+    else
+      e = conv ? launch_prep<VARIANT, K, 5>(a, pro, stream) : launch_prep<VARIANT, K, 1>(a, pro, stream);
   } else {
-    e = launch_prep<VARIANT, K, 1>(a, pro, stream);
+    e = conv ? launch_prep<VARIANT, K, 5>(a, pro, stream) : launch_prep<VARIANT, K, 1>(a, pro, stream);
   }
   if (e == hipSuccess) e = configure_lds<&chunk_scan_kernel<VARIANT, K, OutT>>(scan_lds);
   if (e != hipSuccess) return e;

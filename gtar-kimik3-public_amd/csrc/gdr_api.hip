@@ -87,10 +87,22 @@ int check_rows16(const gdr_tensor& t, const char* name) {
 
 // The prologue of gdr_chunk_fwd_fused (no pointer dereferenced).
 int check_prologue(const gdr_args* a, const gdr_prologue* pro) {
-  if (pro->flags & ~(GDR_PRO_NORM_QK | GDR_PRO_BETA_LOGITS | GDR_PRO_GATE_LOWRANK))
+  if (pro->flags & ~(GDR_PRO_NORM_QK | GDR_PRO_BETA_LOGITS | GDR_PRO_GATE_LOWRANK | GDR_PRO_CONV))
     return fail(GDR_ERR_INVALID, "unknown prologue flags 0x%x", pro->flags);
   if ((pro->flags & GDR_PRO_BETA_LOGITS) && a->variant == GDR_GLA)
     return fail(GDR_ERR_INVALID, "GLA takes no beta (GDR_PRO_BETA_LOGITS)");
+  if (pro->flags & GDR_PRO_CONV) {
+    if (pro->conv_size != 4)
+      return fail(GDR_ERR_UNSUPPORTED, "in-kernel convolution of width %d not supported (4; gdr_short_conv_fwd takes "
+                  "2 to 8)", pro->conv_size);
+    const char* names[] = {"q", "k", "v"};
+    for (int i = 0; i < 3; ++i) {
+      if (!pro->conv_weight[i] || reinterpret_cast<uintptr_t>(pro->conv_weight[i]) % 16)
+        return fail(GDR_ERR_INVALID, "conv_weight[%d] (%s): null or not 16-byte aligned", i, names[i]);
+      if (pro->conv_state_out[i] && pro->conv_state_out[i] == pro->conv_state_in[i])
+        return fail(GDR_ERR_INVALID, "conv_state_out[%d] must not alias conv_state_in[%d]", i, i);
+    }
+  }
   if (!(pro->flags & GDR_PRO_GATE_LOWRANK)) return GDR_OK;
   if (a->variant != GDR_KDA && a->variant != GDR_GLA)
     return fail(GDR_ERR_UNSUPPORTED, "the low-rank gate is for the per-channel gates (KDA, GLA)");
@@ -255,6 +267,39 @@ int gdr_short_conv_fwd(const gdr_conv_args* a, hipStream_t stream) {
   if (a->state_out && a->state_out == a->state_in) return fail(GDR_ERR_INVALID, "state_out must not alias state_in");
   hipError_t e = gdr::launch_short_conv(*a, stream);
   if (e != hipSuccess) return fail(GDR_ERR_HIP, "short convolution launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
+int gdr_norm_gate_fwd(const gdr_norm_gate_args* a, hipStream_t stream) {
+  if (!a) return fail(GDR_ERR_INVALID, "args is NULL");
+  if (a->abi_version != GDR_ABI_VERSION)
+    return fail(GDR_ERR_INVALID, "abi_version %d, library implements %d", a->abi_version, GDR_ABI_VERSION);
+  if (a->batch < 1 || a->seq_len < 0 || a->heads < 1)
+    return fail(GDR_ERR_INVALID, "bad sizes B=%d T=%d H=%d", a->batch, a->seq_len, a->heads);
+  if (a->value_dim < 64 || a->value_dim > 256 || a->value_dim % 64)
+    return fail(GDR_ERR_UNSUPPORTED, "value dim %d not supported (64, 128, 192 or 256)", a->value_dim);
+  if (!(a->eps >= 0.f)) return fail(GDR_ERR_INVALID, "eps must be >= 0");
+  int rc;
+  if ((rc = check_view(a->x, "x", true, false)) || (rc = check_view(a->gate, "gate", true, false)) ||
+      (rc = check_view(a->out, "out", true, false)))
+    return rc;
+  if (a->gate.dtype != a->x.dtype) return fail(GDR_ERR_UNSUPPORTED, "gate must have x's dtype");
+  if (a->weight_dtype != GDR_F32 && a->weight_dtype != a->x.dtype)
+    return fail(GDR_ERR_UNSUPPORTED, "weight must be f32 or x's dtype");
+  const int want_out = a->weight_dtype == GDR_F32 ? GDR_F32 : a->x.dtype;
+  if (a->out.dtype != want_out) return fail(GDR_ERR_UNSUPPORTED, "out dtype must be %d (type promotion)", want_out);
+  if (!a->weight) return fail(GDR_ERR_INVALID, "weight: null pointer");
+  const gdr_tensor* views[] = {&a->x, &a->gate, &a->out};
+  const char* names[] = {"x", "gate", "out"};
+  for (int i = 0; i < 3; ++i) {
+    const int es = elem_size(views[i]->dtype);
+    if (reinterpret_cast<uintptr_t>(views[i]->ptr) % 4 || (views[i]->stride_b * es) % 4 ||
+        (views[i]->stride_h * es) % 4 || (views[i]->stride_t * es) % 4)
+      return fail(GDR_ERR_INVALID, "%s: base pointer and b/h/t strides must be 4-byte aligned", names[i]);
+  }
+  hipError_t e = gdr::launch_norm_gate(*a, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "norm-gate launch failed: %s", hipGetErrorString(e));
   g_last_error.clear();
   return GDR_OK;
 }

@@ -10,7 +10,11 @@ and then calls `chunk_kimi_delta_attention` (:51-55).  The fp32 gate is the op's
 and head at K = 128), written by the layer and read back by the op.  Here the op takes the rank-R activations
 z = decay_proj[0](x) instead (R bf16 values per token, shared by all heads), together with decay_proj[1]'s weight
 and bias and A_log, and computes the gate inside the kernel on MFMA; it also normalises q and k and applies the
-beta sigmoid there.  Gradients are not provided: training keeps the unfused op, which is differentiable.
+beta sigmoid there.  With `conv_weights`, q, k and v are the short convolutions' inputs (q_proj(x), k_proj(x),
+v_proj(x)) and the kernel also applies the three depthwise convolutions of width 4 and their SiLU
+(ShortConvolution, src/layers/short_convolution.py:11-20), reading each sequence's conv state and, like the
+reference's cache path (:16-19), updating it in place.  Gradients are not provided: training keeps the unfused op,
+which is differentiable.
 """
 
 from __future__ import annotations
@@ -26,12 +30,17 @@ def _aligned16(x: torch.Tensor) -> torch.Tensor:
 
 
 def _fused(variant, query, key, value, gate_lowrank, gate_weight, gate_bias, a_log, beta, scale, initial_state,
-           output_final_state, cu_seqlens, normalize_qk, beta_logits):
+           output_final_state, cu_seqlens, normalize_qk, beta_logits, conv_weights=None, conv_states=None):
     name = _VARIANT_NAMES[variant] + " (fused prologue)"
-    if _wants_grad(query, key, value, gate_lowrank, gate_weight, gate_bias, a_log, beta, initial_state):
+    conv_weights = tuple(conv_weights) if conv_weights is not None else None
+    conv_states = tuple(conv_states) if conv_states is not None else None
+    if conv_states is not None and conv_weights is None:
+        raise ValueError(f"{name}: conv_states needs conv_weights")
+    if _wants_grad(query, key, value, gate_lowrank, gate_weight, gate_bias, a_log, beta, initial_state,
+                   *(conv_weights or ())):
         raise NotImplementedError(f"{name}: no backward; train with the unfused chunk op, which has one")
     tensors = [t for t in (query, key, value, gate_lowrank, gate_weight, gate_bias, a_log, beta, initial_state,
-                           cu_seqlens) if t is not None]
+                           cu_seqlens, *(conv_weights or ()), *(conv_states or ())) if t is not None]
     if not all(t.is_cuda for t in tensors):
         raise ValueError(f"{name}: all tensors must be on the GPU (this implementation has no CPU path)")
     device = query.device
@@ -83,6 +92,28 @@ def _fused(variant, query, key, value, gate_lowrank, gate_weight, gate_bias, a_l
             raise ValueError(f"{name}: initial_state must have shape {state_shape}, got {tuple(initial_state.shape)}")
         initial_state = initial_state.float().contiguous()
 
+    conv_w = states_in = states_out = None
+    if conv_weights is not None:
+        if len(conv_weights) != 3:
+            raise ValueError(f"{name}: conv_weights must hold the q, k and v convolution weights")
+        channels = (heads * key_dim, heads * key_dim, heads * value_dim)
+        conv_w = []
+        for wt, ch, nm in zip(conv_weights, channels, "qkv"):
+            wt = wt.reshape(wt.shape[0], -1) if wt.dim() == 3 else wt
+            if tuple(wt.shape) != (ch, 4):
+                raise ValueError(f"{name}: {nm} conv weight must be [{ch}, 4] (or [{ch}, 1, 4]): the in-kernel "
+                                 f"convolution has width 4; got {tuple(conv_weights[len(conv_w)].shape)}")
+            conv_w.append(_aligned16(wt.to(torch.bfloat16).contiguous()))
+        if conv_states is not None:
+            if len(conv_states) != 3:
+                raise ValueError(f"{name}: conv_states must hold the q, k and v conv states")
+            states_in = []
+            for st, ch, nm in zip(conv_states, channels, "qkv"):
+                if tuple(st.shape) != (n_states, ch, 3):
+                    raise ValueError(f"{name}: {nm} conv state must be [{n_states}, {ch}, 3], got {tuple(st.shape)}")
+                states_in.append(st.to(torch.bfloat16).contiguous())
+            states_out = [st.clone() for st in states_in]  # a sequence of length 0 keeps its state
+
     out = torch.empty(batch, heads, seq_len, value_dim, device=device, dtype=out_dtype)
     final_state = torch.empty(state_shape, device=device, dtype=torch.float32) if output_final_state else None
     args = _lib.make_args(variant, query, key, value, None, beta, out, scale, initial_state, final_state, cu_seqlens)
@@ -92,8 +123,13 @@ def _fused(variant, query, key, value, gate_lowrank, gate_weight, gate_bias, a_l
         flags |= _lib.PRO_NORM_QK
     if beta is not None and beta_logits:
         flags |= _lib.PRO_BETA_LOGITS
-    pro = _lib.make_prologue(flags, z, w, bias, a_log)
+    if conv_w is not None:
+        flags |= _lib.PRO_CONV
+    pro = _lib.make_prologue(flags, z, w, bias, a_log, conv_w, states_in, states_out)
     _lib.launch_fused(args, pro, device)
+    if states_out is not None:
+        for st, new in zip(conv_states, states_out):
+            st.copy_(new)
     return (out, final_state) if output_final_state else out
 
 
@@ -113,13 +149,18 @@ def chunk_kimi_delta_attention_fused(
     cu_seqlens: torch.Tensor | None = None,
     normalize_qk: bool = True,
     beta_logits: bool = True,
+    conv_weights=None,
+    conv_states=None,
 ):
     """KDA prefill from the layer's pre-op tensors: q, k [B,H,T,K] before F.normalize (when `normalize_qk`),
     v [B,H,T,V], the gate's rank-R activations `gate_lowrank` [B,T,R] = decay_proj[0](x), `gate_weight` [H*K, R]
     and `gate_bias` [H*K] of decay_proj[1], `a_log` [H], and `beta` [B,H,T] as logits (when `beta_logits`).
+    With `conv_weights` (the q, k, v ShortConvolution weights, [C, 1, 4] each), q, k, v are the convolutions'
+    inputs; `conv_states` (three [N, C, 3] tensors, N sequences) are read and then updated in place.
     Returns what chunk_kimi_delta_attention returns for the prepared inputs."""
     return _fused(_lib.KDA, query, key, value, gate_lowrank, gate_weight, gate_bias, a_log, beta, scale,
-                  initial_state, output_final_state, cu_seqlens, normalize_qk, beta_logits)
+                  initial_state, output_final_state, cu_seqlens, normalize_qk, beta_logits, conv_weights,
+                  conv_states)
 
 
 @torch.compiler.disable
@@ -136,7 +177,10 @@ def chunk_gated_linear_attention_fused(
     output_final_state: bool = False,
     cu_seqlens: torch.Tensor | None = None,
     normalize_qk: bool = False,
+    conv_weights=None,
+    conv_states=None,
 ):
-    """GLA prefill with the same low-rank gate computed in the kernel (no beta)."""
+    """GLA prefill with the same low-rank gate (and optionally the same short convolutions) computed in the kernel
+    (no beta)."""
     return _fused(_lib.GLA, query, key, value, gate_lowrank, gate_weight, gate_bias, a_log, None, scale,
-                  initial_state, output_final_state, cu_seqlens, normalize_qk, False)
+                  initial_state, output_final_state, cu_seqlens, normalize_qk, False, conv_weights, conv_states)

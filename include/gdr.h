@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GDR_ABI_VERSION 6
+#define GDR_ABI_VERSION 7
 
 typedef enum gdr_variant { GDR_KDA = 0, GDR_GDN = 1, GDR_GLA = 2, GDR_DELTANET = 3 } gdr_variant;
 
@@ -96,6 +96,10 @@ int gdr_chunk_fwd(const gdr_args* args, hipStream_t stream);
 #define GDR_PRO_GATE_LOWRANK 4 /* KDA, GLA: gate = -exp(a_log[h]) * softplus(z W[h]^T + bias[h]) in the kernel,
                                   from the rank-R activations z of the gate's first projection; args->gate must
                                   be NULL */
+#define GDR_PRO_CONV 8         /* q, k, v are the short convolutions' inputs (q_proj(x), k_proj(x), v_proj(x)): the
+                                  kernel applies each depthwise causal convolution of width 4 and the SiLU
+                                  (ShortConvolution, src/layers/short_convolution.py:11-20) before the
+                                  normalisation, with each sequence's conv state */
 typedef struct gdr_prologue {
   int32_t flags;            /* GDR_PRO_* bits */
   int32_t rank;             /* R: width of z, a multiple of 32 up to 512 (GATE_LOWRANK) */
@@ -103,6 +107,15 @@ typedef struct gdr_prologue {
   const void* gate_weight;  /* [H * K, R] bf16 row-major, 16-byte aligned: decay_proj[1].weight */
   const float* gate_bias;   /* [H * K] f32, 16-byte aligned, or NULL: decay_proj[1].bias */
   const float* a_log;       /* [H] f32: A_log */
+  int32_t conv_size;        /* CONV: the convolutions' width W; must be 4 */
+  int32_t conv_reserved;
+  const void* conv_weight[3];    /* CONV: q, k, v weights [H * D, W] bf16 (nn.Conv1d weight [C, 1, W]), 16-byte
+                                    aligned; D = K for q, k and V for v */
+  const void* conv_state_in[3];  /* CONV: [N, H * D, W - 1] bf16, the W - 1 inputs before each sequence, or NULL
+                                    (zeros) */
+  void* conv_state_out[3];       /* CONV: [N, H * D, W - 1] bf16, the last W - 1 inputs of each sequence, or NULL;
+                                    must not alias conv_state_in.  A sequence of length 0 leaves its entry
+                                    untouched. */
 } gdr_prologue;
 
 /* gdr_chunk_fwd with the fused prologue `pro`.  Replaces the layer-side q/k normalisation, beta sigmoid and gate
@@ -225,6 +238,31 @@ typedef struct gdr_conv_args {
  * (src/layers/short_convolution.py:11-20), whose padded conv runs across the batch layout and has no notion of packed
  * sequences (:9, :15), including its conv-state path (:16-19). */
 int gdr_short_conv_fwd(const gdr_conv_args* args, hipStream_t stream);
+
+/* Output epilogue of the KDA layer: out = weight * rmsnorm(x) * silu(gate) over each (token, head) row of V
+ * values, where rmsnorm(x) = x / sqrt(mean(x^2) + eps) computed in fp32 and rounded to x's dtype, silu(gate) is
+ * rounded to gate's dtype, and the products are taken in out's dtype (f32 when the weight is f32, as PyTorch's type
+ * promotion gives; else x's dtype, rounded after each product). */
+typedef struct gdr_norm_gate_args {
+  int32_t abi_version;       /* must equal GDR_ABI_VERSION */
+  int32_t batch;             /* B */
+  int32_t seq_len;           /* T */
+  int32_t heads;             /* H */
+  int32_t value_dim;         /* V: 64, 128, 192 or 256 */
+  int32_t weight_dtype;      /* gdr_dtype of weight: GDR_F32 or x's dtype */
+  float eps;
+  int32_t reserved;
+  gdr_tensor x;              /* [B, T, H, V] view of the op's output (stride_b, stride_t, stride_h; unit stride
+                                along V, 4-byte aligned rows): bf16, f16 or f32 */
+  gdr_tensor gate;           /* [B, T, H, V] view of the output gate's pre-activation, x's dtype */
+  gdr_tensor out;            /* [B, T, H, V] view: f32 when weight_dtype is GDR_F32, else x's dtype */
+  const void* weight;        /* [V]: the RMSNorm weight */
+} gdr_norm_gate_args;
+
+/* Replaces `self.norm(out.transpose(1, 2)) * F.silu(self.output_gate_proj(x).view(...))` of
+ * KimiDeltaAttention.forward (src/layers/kimi_delta_attention.py:58-59; RMSNorm src/layers/rmsnorm.py:11-16) with one
+ * HBM-bound pass; the gate's two projections stay with the caller (GEMMs). */
+int gdr_norm_gate_fwd(const gdr_norm_gate_args* args, hipStream_t stream);
 
 /* Thread-local description of the calling thread's last failure ("" if none).  No reference counterpart:
  * the reference surfaces failures as Python exceptions raised by Triton. */

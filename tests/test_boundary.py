@@ -44,7 +44,8 @@ def test_struct_layout_matches_header(tmp_path):
     lines += ['printf("g.size %zu\\n", sizeof(gdr_grads));']
     lines += [f'printf("p.{f} %zu\\n", offsetof(gdr_prologue, {f}));' for f, _ in lib.GdrPrologue._fields_]
     lines += ['printf("p.size %zu\\n", sizeof(gdr_prologue));']
-    for tag, struct, cls in (("a", "gdr_attention_args", lib.GdrAttentionArgs), ("c", "gdr_conv_args", lib.GdrConvArgs)):
+    for tag, struct, cls in (("a", "gdr_attention_args", lib.GdrAttentionArgs), ("c", "gdr_conv_args", lib.GdrConvArgs),
+                             ("n", "gdr_norm_gate_args", lib.GdrNormGateArgs)):
         lines += [f'printf("{tag}.{f} %zu\\n", offsetof({struct}, {f}));' for f, _ in cls._fields_]
         lines += [f'printf("{tag}.size %zu\\n", sizeof({struct}));']
     lines += ["return 0; }"]
@@ -66,7 +67,7 @@ def test_struct_layout_matches_header(tmp_path):
     for f, _ in lib.GdrPrologue._fields_:
         assert int(offsets["p." + f]) == getattr(lib.GdrPrologue, f).offset, f
     assert int(offsets["p.size"]) == ctypes.sizeof(lib.GdrPrologue)
-    for tag, cls in (("a", lib.GdrAttentionArgs), ("c", lib.GdrConvArgs)):
+    for tag, cls in (("a", lib.GdrAttentionArgs), ("c", lib.GdrConvArgs), ("n", lib.GdrNormGateArgs)):
         for f, _ in cls._fields_:
             assert int(offsets[f"{tag}.{f}"]) == getattr(cls, f).offset, f
         assert int(offsets[f"{tag}.size"]) == ctypes.sizeof(cls)
@@ -206,9 +207,22 @@ def test_fused_prologue_rejects_bad_arguments_without_a_gpu():
     assert so.gdr_chunk_fwd_fused(ctypes.byref(args), None, None) == -1
     assert b"prologue" in so.gdr_last_error()
     pro = lib.GdrPrologue()
-    pro.flags = 8
+    pro.flags = 16
     assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -1
     assert b"flags" in so.gdr_last_error()
+    pro.flags = lib.PRO_CONV
+    pro.conv_size = 3  # the in-kernel convolution has width 4
+    assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -2
+    assert b"width 3" in so.gdr_last_error()
+    pro.conv_size = 4
+    pro.conv_weight[0], pro.conv_weight[1] = 4096, 8192  # v's weight missing
+    assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -1
+    assert b"conv_weight[2]" in so.gdr_last_error()
+    pro.conv_weight[2] = 12288
+    pro.conv_state_in[1] = pro.conv_state_out[1] = 65536
+    assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -1
+    assert b"alias" in so.gdr_last_error()
+    pro = lib.GdrPrologue()
     pro.flags = lib.PRO_GATE_LOWRANK
     pro.rank = 48
     assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -2
@@ -271,3 +285,38 @@ def test_stack_ops_refuse_cpu_tensors_and_gradients():
         gdr.flash_attention(q.requires_grad_(), q, q)
     with pytest.raises(ValueError, match="GPU"):
         gdr.short_convolution(torch.randn(1, 8, 64), torch.randn(64, 1, 4))
+
+
+def test_norm_gate_rejects_bad_arguments_without_a_gpu():
+    so = lib.load_library()
+    a = lib.GdrNormGateArgs()
+    a.abi_version = lib.ABI_VERSION
+    a.batch, a.seq_len, a.heads, a.value_dim, a.eps = 1, 4, 2, 96, 1e-6
+    for name, off in (("x", 256), ("gate", 1024), ("out", 2048)):
+        view = getattr(a, name)
+        view.ptr, view.dtype = off, lib.BF16
+    a.weight, a.weight_dtype = 4096, lib.F32
+    assert so.gdr_norm_gate_fwd(ctypes.byref(a), None) == -2
+    assert b"value dim 96" in so.gdr_last_error()
+    a.value_dim = 128
+    assert so.gdr_norm_gate_fwd(ctypes.byref(a), None) == -2  # f32 weight: out must be f32
+    assert b"type promotion" in so.gdr_last_error()
+    a.out.dtype = lib.F32
+    a.gate.dtype = lib.F16
+    assert so.gdr_norm_gate_fwd(ctypes.byref(a), None) == -2
+    assert b"gate must have x's dtype" in so.gdr_last_error()
+    a.gate.dtype = lib.BF16
+    a.x.ptr = 258  # rows are read 4 bytes at a time
+    assert so.gdr_norm_gate_fwd(ctypes.byref(a), None) == -1
+    assert b"4-byte aligned" in so.gdr_last_error()
+
+
+def test_norm_gate_and_fused_conv_refuse_cpu_tensors():
+    x = torch.randn(1, 4, 2, 128)
+    with pytest.raises(ValueError, match="GPU"):
+        gdr.output_norm_gate(x, x, torch.ones(128))
+    q, k, v, g, b = _cpu_inputs()
+    z, w, a_log = torch.randn(1, 8, 32), torch.randn(2 * 64, 32), torch.zeros(2)
+    cw = [torch.randn(128, 1, 4)] * 3
+    with pytest.raises(ValueError, match="GPU"):
+        gdr.chunk_kimi_delta_attention_fused(q, k, v, z, w, None, a_log, b, conv_weights=cw)
