@@ -245,10 +245,45 @@ def bench_fused(gdr, torch, steps, warmup):
         return gdr.chunk_kimi_delta_attention(qn, kn, v, gate.transpose(1, 2), logits.sigmoid(), initial_state=h0,
                                               output_final_state=True)
 
+    # with the short convolutions: q, k, v are the convolutions' inputs [B, T, C] and the kernel convolves
+    C = H * K
+    xq, xk, xv = (x.transpose(1, 2).contiguous().view(B, T, C) for x in (q, k, v))
+    bound = 1 / math.sqrt(4)
+    cw = [((torch.rand(C, 1, 4, generator=gen) * 2 - 1) * bound).bfloat16().to(dev) for _ in range(3)]
+    heads = lambda x: x.view(B, T, H, -1).transpose(1, 2)
+
+    def fused_conv():
+        return gdr.chunk_kimi_delta_attention_fused(heads(xq), heads(xk), heads(xv), z, w, bias, a_log, logits,
+                                                    initial_state=h0, output_final_state=True, conv_weights=cw)
+
+    def torch_conv_unfused():  # ShortConvolution (src/layers/short_convolution.py:11-15), the preparation, the op
+        conv = lambda x, wt: F.silu(F.conv1d(x.transpose(1, 2), wt, padding=3, groups=C)[..., :T]).transpose(1, 2)
+        qc, kc, vc = (heads(conv(x, wt)) for x, wt in zip((xq, xk, xv), cw))
+        qn = F.normalize(qc.float(), dim=-1).bfloat16()
+        kn = F.normalize(kc.float(), dim=-1).bfloat16()
+        gate = -a_log.exp()[:, None] * F.softplus(F.linear(z, w, bias.bfloat16()).float().view(B, T, H, K))
+        return gdr.chunk_kimi_delta_attention(qn, kn, vc, gate.transpose(1, 2), logits.sigmoid(), initial_state=h0,
+                                              output_final_state=True)
+
+    # the output epilogue on the op's output: RMSNorm x SiLU gate (src/layers/kimi_delta_attention.py:58-59)
+    ogate = torch.randn(B, T, H, V, generator=gen).bfloat16().to(dev)
+    nweight = torch.ones(V, device=dev)
+
+    def norm_gate():
+        return gdr.output_norm_gate(o_out.transpose(1, 2), ogate, nweight, 1e-6)
+
+    def torch_norm_gate():
+        x = o_out.transpose(1, 2)
+        xf = x.float()
+        return nweight * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(x.dtype) * F.silu(ogate)
+
     stream = torch.cuda.current_stream()
     res = {}
     with torch.no_grad():
-        for name, fn in (("fused", fused), ("torch_prologue_plus_op", unfused)):
+        o_out = fused()[0]
+        for name, fn in (("fused", fused), ("torch_prologue_plus_op", unfused), ("fused_conv", fused_conv),
+                         ("torch_conv_prologue_plus_op", torch_conv_unfused), ("norm_gate", norm_gate),
+                         ("torch_norm_gate", torch_norm_gate)):
             for _ in range(warmup):
                 fn()
             torch.cuda.synchronize()
@@ -263,6 +298,9 @@ def bench_fused(gdr, torch, steps, warmup):
     gbs = nbytes / (res["fused"] * 1e-3) / 1e9
     return {"workload": "kda_chunk_prefill_fused_prologue", **{x: cfg[x] for x in ("B", "T", "H", "K", "V", "R")},
             "ms_fused": round(res["fused"], 4), "ms_torch_prologue_plus_op": round(res["torch_prologue_plus_op"], 4),
+            "ms_fused_with_conv": round(res["fused_conv"], 4),
+            "ms_torch_conv_prologue_plus_op": round(res["torch_conv_prologue_plus_op"], 4),
+            "us_norm_gate": round(res["norm_gate"] * 1e3, 2), "us_torch_norm_gate": round(res["torch_norm_gate"] * 1e3, 2),
             "tokens_per_s": round(B * T / (res["fused"] * 1e-3), 1), "algorithmic_bytes": nbytes,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4)}}
@@ -325,8 +363,9 @@ def bench_stack(gdr, workloads, torch, steps, warmup):
                       f"{cfg.num_layers // cfg.attention_interval} attention)",
             "hidden": cfg.hidden_size, "ms_per_forward": round(total, 3), "tokens_per_s": round(tokens / (total * 1e-3), 1),
             "kda_op_ms": round(kda, 3), "kda_op_share": round(kda / total, 4),
-            "note": "random bf16 weights; projections, norms and MLP in PyTorch; KDA, attention and short convolution "
-                    "on this package's kernels"}
+            "note": "random bf16 weights; projections, block norms and MLP in PyTorch; attention, the KDA op with its "
+                    "short convolutions and prologue fused in (kda_op_ms), and the KDA output norm-gate on this "
+                    "package's kernels"}
 
 
 def train_bytes(B, T, H, K, V, **_):

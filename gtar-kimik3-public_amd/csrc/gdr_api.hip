@@ -279,6 +279,8 @@ int gdr_norm_gate_fwd(const gdr_norm_gate_args* a, hipStream_t stream) {
     return fail(GDR_ERR_INVALID, "bad sizes B=%d T=%d H=%d", a->batch, a->seq_len, a->heads);
   if (a->value_dim < 64 || a->value_dim > 256 || a->value_dim % 64)
     return fail(GDR_ERR_UNSUPPORTED, "value dim %d not supported (64, 128, 192 or 256)", a->value_dim);
+  if (int64_t(a->batch) * a->seq_len * a->heads >= (int64_t(1) << 31))
+    return fail(GDR_ERR_UNSUPPORTED, "B * T * H must be below 2^31");
   if (!(a->eps >= 0.f)) return fail(GDR_ERR_INVALID, "eps must be >= 0");
   int rc;
   if ((rc = check_view(a->x, "x", true, false)) || (rc = check_view(a->gate, "gate", true, false)) ||
@@ -294,9 +296,9 @@ int gdr_norm_gate_fwd(const gdr_norm_gate_args* a, hipStream_t stream) {
   const char* names[] = {"x", "gate", "out"};
   for (int i = 0; i < 3; ++i) {
     const int es = elem_size(views[i]->dtype);
-    if (reinterpret_cast<uintptr_t>(views[i]->ptr) % 4 || (views[i]->stride_b * es) % 4 ||
-        (views[i]->stride_h * es) % 4 || (views[i]->stride_t * es) % 4)
-      return fail(GDR_ERR_INVALID, "%s: base pointer and b/h/t strides must be 4-byte aligned", names[i]);
+    if (reinterpret_cast<uintptr_t>(views[i]->ptr) % 16 || (views[i]->stride_b * es) % 16 ||
+        (views[i]->stride_h * es) % 16 || (views[i]->stride_t * es) % 16)
+      return fail(GDR_ERR_INVALID, "%s: base pointer and b/h/t strides must be 16-byte aligned", names[i]);
   }
   hipError_t e = gdr::launch_norm_gate(*a, stream);
   if (e != hipSuccess) return fail(GDR_ERR_HIP, "norm-gate launch failed: %s", hipGetErrorString(e));

@@ -37,7 +37,7 @@ def output_norm_gate(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, 
     weight = weight.contiguous()
     views = []
     for t in (x, gate):
-        if t.stride(-1) != 1 or t.data_ptr() % 4 or any((s * t.element_size()) % 4 for s in t.stride()[:3]):
+        if t.stride(-1) != 1 or t.data_ptr() % 16 or any((s * t.element_size()) % 16 for s in t.stride()[:3]):
             t = t.contiguous()
         views.append(t)
     out_dtype = torch.float32 if weight.dtype == torch.float32 else x.dtype

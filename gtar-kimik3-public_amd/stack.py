@@ -5,9 +5,9 @@ The reference's KimiK3 model (src/models/kimi_k3.py:39-66) stacks blocks whose m
 reference runs it on padded batches; this harness runs the same blocks on packed sequences (`cu_seqlens`) with the
 package's gfx950 ops on the paths that must respect sequence boundaries or carry per-sequence state:
 
-  * KDA mixer (src/layers/kimi_delta_attention.py:41-61): the three short convolutions are `short_convolution`
-    (segment-aware), and normalisation, beta sigmoid, the low-rank gate and the op run as one
-    `chunk_kimi_delta_attention_fused` call with a per-sequence state;
+  * KDA mixer (src/layers/kimi_delta_attention.py:41-61): the three short convolutions (segment-aware), the q/k
+    normalisation, the beta sigmoid, the low-rank gate and the op run as one `chunk_kimi_delta_attention_fused`
+    call with a per-sequence state, and the output RMSNorm x SiLU gate is one `output_norm_gate` pass;
   * attention mixer (src/layers/attention.py:82-117, no rotary embedding, as KimiK3 passes none): `flash_attention`
     over the packed sequences.
 
@@ -25,7 +25,7 @@ import torch
 import torch.nn.functional as F
 
 from .attention import flash_attention
-from .conv import short_convolution
+from .epilogue import output_norm_gate
 from .fused import chunk_kimi_delta_attention_fused
 
 
@@ -96,9 +96,9 @@ class HybridStack:
         T = x.shape[0]
         nh, hd = cfg.kda_num_heads, cfg.kda_head_dim
         shape = (1, T, nh, hd)
-        q = short_convolution(F.linear(x, w["wq"])[None], w["conv_q"], cu_seqlens=cu).view(shape)
-        k = short_convolution(F.linear(x, w["wk"])[None], w["conv_k"], cu_seqlens=cu).view(shape)
-        v = short_convolution(F.linear(x, w["wv"])[None], w["conv_v"], cu_seqlens=cu).view(shape)
+        q = F.linear(x, w["wq"])[None].view(shape)  # the convolutions' inputs: the kernel convolves
+        k = F.linear(x, w["wk"])[None].view(shape)
+        v = F.linear(x, w["wv"])[None].view(shape)
         z = F.linear(x, w["w_decay0"])[None]
         beta = F.linear(x, w["w_beta"]).float()[None]  # logits
         if timed:
@@ -106,13 +106,14 @@ class HybridStack:
             ev[0].record()
         out, state = chunk_kimi_delta_attention_fused(
             q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), z, w["w_decay1"], w["b_decay1"], w["a_log"],
-            beta.transpose(1, 2), initial_state=state, output_final_state=True, cu_seqlens=cu)
+            beta.transpose(1, 2), initial_state=state, output_final_state=True, cu_seqlens=cu,
+            conv_weights=(w["conv_q"], w["conv_k"], w["conv_v"]))
         if timed:
             ev[1].record()
             self.kda_op_events.append(ev)
-        gate = F.silu(F.linear(F.linear(x, w["w_og0"]), w["w_og1"])).view(T, nh, hd)
-        o = rms_norm(out[0].transpose(0, 1), w["norm"], cfg.rms_norm_eps) * gate
-        return F.linear(o.reshape(T, nh * hd), w["wo"]), state
+        gate = F.linear(F.linear(x, w["w_og0"]), w["w_og1"]).view(shape)  # pre-activation
+        o = output_norm_gate(out.transpose(1, 2), gate, w["norm"], cfg.rms_norm_eps)  # [1, T, nh, hd]
+        return F.linear(o.reshape(T, nh * hd).to(x.dtype), w["wo"]), state
 
     def _attention(self, x, w, cu):
         cfg = self.cfg

@@ -253,7 +253,7 @@ typedef struct gdr_norm_gate_args {
   float eps;
   int32_t reserved;
   gdr_tensor x;              /* [B, T, H, V] view of the op's output (stride_b, stride_t, stride_h; unit stride
-                                along V, 4-byte aligned rows): bf16, f16 or f32 */
+                                along V; base and strides 16-byte aligned, as for gate and out): bf16, f16 or f32 */
   gdr_tensor gate;           /* [B, T, H, V] view of the output gate's pre-activation, x's dtype */
   gdr_tensor out;            /* [B, T, H, V] view: f32 when weight_dtype is GDR_F32, else x's dtype */
   const void* weight;        /* [V]: the RMSNorm weight */

@@ -306,9 +306,9 @@ def test_norm_gate_rejects_bad_arguments_without_a_gpu():
     assert so.gdr_norm_gate_fwd(ctypes.byref(a), None) == -2
     assert b"gate must have x's dtype" in so.gdr_last_error()
     a.gate.dtype = lib.BF16
-    a.x.ptr = 258  # rows are read 4 bytes at a time
+    a.x.ptr = 264  # rows are moved in 16-byte words
     assert so.gdr_norm_gate_fwd(ctypes.byref(a), None) == -1
-    assert b"4-byte aligned" in so.gdr_last_error()
+    assert b"16-byte aligned" in so.gdr_last_error()
 
 
 def test_norm_gate_and_fused_conv_refuse_cpu_tensors():
