@@ -61,12 +61,13 @@ struct PrepLds {
   static_assert(4 * 512 <= 11 * K * 4, "AINV alias");
 };
 
-// softplus(x) = max(x, 0) + log1p(e^{-|x|}) in fp32.  log1p(y) for y in (0, 1] as log(u) * y / (u - 1) with u = 1 + y
-// (exact to a few ulp even where u rounds to 1 + y's leading bits: the rounding error of u cancels in the ratio).
+// softplus(x) = max(x, 0) + log1p(e^{-|x|}) in fp32, with two transcendental instructions.  log1p(y), y in (0, 1]:
+// for y > 2^-6 as log(1 + y), whose rounding of 1 + y (2^-24 absolute) is below 2^-18 of the result; below that as
+// the series y - y^2/2 + y^3/3 - y^4/4 + y^5/5, whose truncation is below y^5/6 < 2^-32 of the result.
 __device__ __forceinline__ float softplus_f32(float x) {
   const float y = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e);
-  const float u = 1.f + y;
-  const float l1p = u == 1.f ? y : __builtin_amdgcn_logf(u) * kLn2 * __fdividef(y, u - 1.f);
+  const float series = y * (1.f - y * (0.5f - y * (1.f / 3.f - y * (0.25f - y * 0.2f))));
+  const float l1p = y > 0x1p-6f ? __builtin_amdgcn_logf(1.f + y) * kLn2 : series;
   return fmaxf(x, 0.f) + l1p;
 }
 
