@@ -269,6 +269,9 @@ def bench_fused(gdr, torch, steps, warmup):
     ogate = torch.randn(B, T, H, V, generator=gen).bfloat16().to(dev)
     nweight = torch.ones(V, device=dev)
 
+    def short_conv():  # one standalone segment-free short convolution of the c2 q projection (gdr_short_conv_fwd)
+        return gdr.short_convolution(xq, cw[0])
+
     def norm_gate():
         return gdr.output_norm_gate(o_out.transpose(1, 2), ogate, nweight, 1e-6)
 
@@ -283,7 +286,7 @@ def bench_fused(gdr, torch, steps, warmup):
         o_out = fused()[0]
         for name, fn in (("fused", fused), ("torch_prologue_plus_op", unfused), ("fused_conv", fused_conv),
                          ("torch_conv_prologue_plus_op", torch_conv_unfused), ("norm_gate", norm_gate),
-                         ("torch_norm_gate", torch_norm_gate)):
+                         ("torch_norm_gate", torch_norm_gate), ("short_conv", short_conv)):
             for _ in range(warmup):
                 fn()
             torch.cuda.synchronize()
@@ -301,6 +304,7 @@ def bench_fused(gdr, torch, steps, warmup):
             "ms_fused_with_conv": round(res["fused_conv"], 4),
             "ms_torch_conv_prologue_plus_op": round(res["torch_conv_prologue_plus_op"], 4),
             "us_norm_gate": round(res["norm_gate"] * 1e3, 2), "us_torch_norm_gate": round(res["torch_norm_gate"] * 1e3, 2),
+            "us_short_conv": round(res["short_conv"] * 1e3, 2),
             "tokens_per_s": round(B * T / (res["fused"] * 1e-3), 1), "algorithmic_bytes": nbytes,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4)}}
