@@ -58,6 +58,7 @@ struct PrepLds {
   static constexpr int NRM = BETA + 256;          // fp32 [2][64]   fused prologue: 1 / ||q||, 1 / ||k|| per row
   static constexpr int BYTES = NRM + 512;
   static_assert(8 * K * 4 <= 16 * 512, "EPRE/ETAIL alias");
+  static_assert(SC + 64 * K * 2 <= FAR, "fused prologue: the z staging block [64][K] fits in SC .. RDS");
   static_assert(4 * 512 <= 11 * K * 4, "AINV alias");
 };
 
@@ -135,33 +136,52 @@ __device__ __forceinline__ float conv4_silu1(const __bf16* x0, int64_t x_st, int
 // The low-rank gate of the fused prologue for the chunk's 64 rows:
 //   g[t][c] = -e^{A_log[h]} softplus(z_t . W[h K + c] + bias[h K + c])
 // Wave w computes channels [w K / 4, (w + 1) K / 4) of all 64 rows as Gᵀ = W_h Zᵀ on v_mfma_f32_16x16x32_bf16 (A = 16
-// channels x 32 of R from W's rows, B = 32 of R x 16 tokens from z's rows), so each wave reads only its quarter of W
-// (the rows of z are shared through L2).  Lane (l16, g4) ends with channels 16 t + 4 g4 + i of token 16 j + l16; the
-// values go to the fp32 LDS rows `gst` (row pitch K + 4), from which every lane later reads its own row.
+// channels x 32 of R from W's rows, B = 32 of R x 16 tokens from z's rows), so each wave reads only its quarter of W.
+// z goes through LDS once per workgroup, K of R at a time (`zs`, [64][K] bf16, 16-byte chunk c of row r stored at
+// chunk c ^ (r mod K / 8), copied with global_load_lds_dwordx4: the permutation is applied to the source addresses,
+// since the copy lands lane i at base + 16 i).  Lane (l16, g4) ends with channels 16 t + 4 g4 + i of token 16 j + l16;
+// the values go to the fp32 LDS rows `gst` (row pitch K + 4), from which every lane later reads its own row.
 template <int K>
 __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h, const __bf16* zchunk, int64_t z_st,
-                                                  int last_row, float* gst, int wave, int l16, int g4) {
-  constexpr int CT = K / 64;  // 16-channel tiles per wave
-  const int R = pro.rank, ch0 = wave * (K / 4);
+                                                  int last_row, float* gst, __bf16* zs, int wave, int l16, int g4) {
+  constexpr int CT = K / 64;          // 16-channel tiles per wave
+  constexpr int RB = K, C16 = RB / 8;  // R per LDS block, 16-byte chunks per staged row
+  const int R = pro.rank, ch0 = wave * (K / 4), lane = threadIdx.x & 63;
   const __bf16* w = static_cast<const __bf16*>(pro.gate_weight) + (size_t(h) * K + ch0 + l16) * R + 8 * g4;
-  const __bf16* zr[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) zr[j] = zchunk + int64_t(min(16 * j + l16, last_row)) * z_st + 8 * g4;
   floatx4 acc[CT][4];
 #pragma unroll
   for (int t = 0; t < CT; ++t)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[t][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < R / 32; ++s) {  // the accumulators start at zero right before this loop
-    bf16x8 zb[4];
+  for (int r0 = 0; r0 < R; r0 += RB) {  // the accumulators start at zero right before this loop
+    // stage z[0:64][r0 : r0 + RB] (columns past R read column R - 8 and meet zero W operands below)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) zb[j] = *reinterpret_cast<const bf16x8*>(zr[j] + 32 * s);
-#pragma unroll
-    for (int t = 0; t < CT; ++t) {
-      const bf16x8 wa = *reinterpret_cast<const bf16x8*>(w + size_t(16 * t) * R + 32 * s);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[t][j] = mfma32(wa, zb[j], acc[t][j]);
+    for (int k = 0; k < 64 * C16 / 256; ++k) {
+      const int slot = 64 * (4 * k + wave) + lane;  // LDS chunk index: row slot / C16, chunk slot % C16
+      const int row = slot / C16, c = (slot % C16) ^ (row % C16);
+      const int col = min(r0 + 8 * c, R - 8);
+      lds_dma16(zchunk + int64_t(min(row, last_row)) * z_st + col, zs + 8 * 64 * (4 * k + wave));
     }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < RB / 32; ++s) {
+      const bool live = r0 + 32 * s < R;
+      bf16x8 zb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = 16 * j + l16, c = (4 * s + g4) ^ (row % C16);
+        zb[j] = *reinterpret_cast<const bf16x8*>(zs + row * RB + 8 * c);
+      }
+#pragma unroll
+      for (int t = 0; t < CT; ++t) {
+        bf16x8 wa = *reinterpret_cast<const bf16x8*>(w + size_t(16 * t) * R + min(r0 + 32 * s, R - 32));
+        if (!live) wa = bf16x8{};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[t][j] = mfma32(wa, zb[j], acc[t][j]);
+      }
+    }
+    __syncthreads();  // every wave is done with this block of zs
   }
   const float neg_a = -__builtin_amdgcn_exp2f(pro.a_log[h] * kLog2e);
 #pragma unroll
@@ -320,7 +340,7 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
     const __bf16* zchunk = static_cast<const __bf16*>(pro.gate_lowrank.ptr) + bidx * pro.gate_lowrank.stride_b +
                            int64_t(bos + c * kChunk) * pro.gate_lowrank.stride_t;
     lowrank_gate_rows<K>(pro, h, zchunk, pro.gate_lowrank.stride_t, len - 1 - c * kChunk,
-                         reinterpret_cast<float*>(smem), wave, l16, g4);
+                         reinterpret_cast<float*>(smem), reinterpret_cast<__bf16*>(smem + L::SC), wave, l16, g4);
     __syncthreads();
   }
   if constexpr (kConv) {
