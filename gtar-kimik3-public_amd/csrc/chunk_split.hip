@@ -755,6 +755,7 @@ constexpr int kScanTiles = 1;                          // 16-column tiles per co
 constexpr int kScanCompute = kScanSlice / (16 * kScanTiles);  // compute waves per scan workgroup
 constexpr int kScanLoaders = 4;                        // loader waves per scan workgroup
 constexpr int kScanThreads = 64 * (kScanCompute + kScanLoaders);
+constexpr int kOP = kScanSlice + 8;  // row pitch (elements) of the scan's output tile in LDS
 
 // kStates (backward recompute): instead of the output, write the fp32 state entering every chunk (and the final
 // one) to `states` [NC + 1][K][V] and the bf16 u to `ubuf` [NC * 64][V], per (sequence, head).
@@ -860,9 +861,27 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
           states[st_base + (size_t(c) * K + 16 * m + 4 * g4 + r) * V + c0 + 16 * t + l16] = st[t][m][r];
   };
 
+  // The output of a chunk goes through LDS: the compute waves write their 16-column stripes into the chunk's tile
+  // (double-buffered, [64][kOP]), and after the step's barrier wave w stores rows 16 w .. 16 w + 15 of the previous
+  // chunk as whole 64-column rows with 16-byte stores (instead of 16 row pieces of 32 bytes per store).
+  OutT* otile = reinterpret_cast<OutT*>(smem + 2 * SB);
+  auto store_tile = [&](int chunk) {
+    constexpr int kPer = 16 / int(sizeof(OutT)), kRowPieces = kScanSlice / kPer, kRows = 64 / kRowPieces;
+    const OutT* tl = otile + (chunk & 1) * 64 * kOP;
+#pragma unroll
+    for (int u = 0; u < 16 / kRows; ++u) {
+      const int row = 16 * wave + kRows * u + lane / kRowPieces, pc = lane % kRowPieces;
+      const uint4 v = *reinterpret_cast<const uint4*>(tl + row * kOP + pc * kPer);
+      const int tk = chunk * kChunk + row;
+      if (tk < len) *reinterpret_cast<uint4*>(op + tk * o_st + v0 + pc * kPer) = v;
+    }
+  };
   for (int s = 0; s < nchunks; ++s) {
     const unsigned char* bb = smem + (s & 1) * SB;
     if constexpr (kStates) store_state(s);
+    if constexpr (!kStates) {
+      if (s > 0) store_tile(s - 1);
+    }
     const __bf16* wl = reinterpret_cast<const __bf16*>(bb + R::W);
     const __bf16* ql = reinterpret_cast<const __bf16*>(bb + R::QD);
     const __bf16* scl = reinterpret_cast<const __bf16*>(bb + R::SC);
@@ -960,16 +979,18 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
 #pragma unroll
         for (int t = 0; t < NT; ++t) st[t][m] = mfma32(fk[m & 1][kk], concat(ub[t][2 * kk], ub[t][2 * kk + 1]), st[t][m]);
     }
-    // output: lane holds O[token 16 i + l16][columns c0 + 16 t + 4 g4 .. + 3]
+    // output: lane holds O[token 16 i + l16][columns c0 + 16 t + 4 g4 .. + 3], into the chunk's LDS tile
+    if constexpr (!kStates) {
+      OutT* tw = otile + (s & 1) * 64 * kOP;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tk = s * kChunk + 16 * i + l16;
-      if (!kStates && tk < len) {
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) store4(op + tk * o_st + c0 + 16 * t + 4 * g4, acc_ot[t][i]);
-      }
+        for (int t = 0; t < NT; ++t) store4(tw + (16 * i + l16) * kOP + (c0 - v0) + 16 * t + 4 * g4, acc_ot[t][i]);
     }
     lds_barrier();
+  }
+  if constexpr (!kStates) {
+    if (nchunks > 0) store_tile(nchunks - 1);
   }
   if constexpr (kStates) store_state(nchunks);
   if (a.ht) {
@@ -1016,7 +1037,8 @@ template <int VARIANT, int K, typename OutT>
 hipError_t launch_split_typed(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
   const int nc = (a.seq_len + kChunk - 1) / kChunk;
   const int64_t rec = Rec<K>::bytes(a.value_dim);
-  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::UT_SLICE);
+  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::UT_SLICE) + 2 * 64 * kOP * int(sizeof(OutT));
+  static_assert(scan_lds <= 160 * 1024, "scan LDS");
   hipError_t e;
   const bool conv = pro.flags & GDR_PRO_CONV;
   if (!pro.flags) {

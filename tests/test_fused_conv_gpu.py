@@ -126,7 +126,7 @@ def _norm_gate_ref(x, gate, weight, eps):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("weight_f32", [True, False])
-@pytest.mark.parametrize("V", [64, 128, 256])
+@pytest.mark.parametrize("V", [64, 128, 192, 256])
 def test_norm_gate_matches_layer_expression(dtype, weight_f32, V):
     B, H, T, eps = 2, 3, 77, 1e-6
     gen = torch.Generator().manual_seed(5)
