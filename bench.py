@@ -187,25 +187,36 @@ def bench_verify(gdr, workloads, torch, warmup):
             _, _, block = gdr.verify_kimi_delta_attention(*ring[i % 8].args(), initial_state=cur[0])
             cur[0] = block.commit(accepted[i % 8])
 
-        for fn in (verify_only, commit_only, cycle):
+        pending = [blocks[0]]
+
+        def one_launch_cycle(i):  # commit of the previous block and verify of this one (gdr_recurrent_commit_verify)
+            _, _, pending[0] = gdr.verify_kimi_delta_attention(*ring[i % 8].args(), pending=pending[0],
+                                                               accepted=accepted[i % 8])
+
+        for fn in (verify_only, commit_only, cycle, one_launch_cycle):
             for i in range(warmup):
                 fn(i)
         torch.cuda.synchronize()
         v_ms = timed(verify_only, cfg["cycles"])
         c_ms = timed(commit_only, cfg["cycles"])
         y_ms = timed(cycle, cfg["cycles"])
+        f_ms = timed(one_launch_cycle, cfg["cycles"])
     mean_accepted = sum(int(c.sum()) for c in counts) / len(counts)
     vb, cb = verify_bytes(**cfg), commit_bytes(mean_accepted, **cfg)
+    fb = vb + cb - B * H * K * V * 4  # one launch reads the state once for both halves
     gbs = lambda nbytes, ms: nbytes / (ms * 1e-3) / 1e9
     return {"workload": "kda_verify_commit", "B": B, "H": H, "K": K, "V": V, "T": T, "cycles": cfg["cycles"],
             "mean_accepted_tokens": round(mean_accepted / B, 3),
             "us_verify": round(v_ms * 1e3, 2), "us_commit": round(c_ms * 1e3, 2), "us_cycle": round(y_ms * 1e3, 2),
             "verify_gbs": round(gbs(vb, v_ms), 1), "commit_gbs": round(gbs(cb, c_ms), 1),
             "accepted_tokens_per_s": round(mean_accepted / (y_ms * 1e-3), 1),
+            "us_cycle_one_launch": round(f_ms * 1e3, 2), "one_launch_gbs": round(gbs(fb, f_ms), 1),
+            "accepted_tokens_per_s_one_launch": round(mean_accepted / (f_ms * 1e-3), 1),
             "roofline": {"bound": "hbm", "achieved": round(gbs(vb + cb, y_ms), 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs(vb + cb, y_ms) / HBM_PEAK_GBS, 4),
                          "traffic_verify": committed_traffic("recurrent_kda_verify"),
-                         "traffic_commit": committed_traffic("recurrent_kda_commit")}}
+                         "traffic_commit": committed_traffic("recurrent_kda_commit"),
+                         "traffic_one_launch": committed_traffic("recurrent_kda_commit_verify")}}
 
 
 def fused_bytes(B, T, H, K, V, R=128, **_):

@@ -158,6 +158,8 @@ EXPORTS = {
     "gdr_recurrent_verify": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p]),
     "gdr_recurrent_commit": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p,
                                             ctypes.c_void_p]),
+    "gdr_recurrent_commit_verify": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p,
+                                                   ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p]),
     "gdr_attention_fwd": (ctypes.c_int, [ctypes.POINTER(GdrAttentionArgs), ctypes.c_void_p]),
     "gdr_short_conv_fwd": (ctypes.c_int, [ctypes.POINTER(GdrConvArgs), ctypes.c_void_p]),
     "gdr_norm_gate_fwd": (ctypes.c_int, [ctypes.POINTER(GdrNormGateArgs), ctypes.c_void_p]),
@@ -295,6 +297,18 @@ def commit(args: GdrArgs, updates: torch.Tensor, accepted: torch.Tensor | None, 
     acc = ctypes.c_void_p(accepted.data_ptr()) if accepted is not None else None
     _check("gdr_recurrent_commit", lib.gdr_recurrent_commit(ctypes.byref(args), ctypes.c_void_p(updates.data_ptr()),
                                                             acc, ctypes.c_void_p(stream)))
+
+
+def commit_verify(prev: GdrArgs, prev_updates: torch.Tensor, accepted: torch.Tensor | None, args: GdrArgs,
+                  updates: torch.Tensor, device: torch.device) -> None:
+    """Enqueue gdr_recurrent_commit_verify: commit `prev` (into prev.ht) and verify `args` from that state, one launch."""
+    lib = load_library()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    acc = ctypes.c_void_p(accepted.data_ptr()) if accepted is not None else None
+    _check("gdr_recurrent_commit_verify",
+           lib.gdr_recurrent_commit_verify(ctypes.byref(prev), ctypes.c_void_p(prev_updates.data_ptr()), acc,
+                                           ctypes.byref(args), ctypes.c_void_p(updates.data_ptr()),
+                                           ctypes.c_void_p(stream)))
 
 
 def make_prologue(flags: int, gate_lowrank=None, gate_weight=None, gate_bias=None, a_log=None, conv_weights=None,

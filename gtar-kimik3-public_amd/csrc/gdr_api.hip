@@ -195,7 +195,10 @@ int gdr_recurrent_verify(const gdr_args* a, float* updates, hipStream_t stream) 
   return GDR_OK;
 }
 
-int gdr_recurrent_commit(const gdr_args* a, const float* updates, const int32_t* accepted, hipStream_t stream) {
+namespace {
+
+// The arguments of a commit: sizes, k, the gate, the state pointers and the record (no pointer dereferenced).
+int check_commit(const gdr_args* a, const float* updates) {
   int rc = check_shape(a, false);
   if (rc) return rc;
   const bool has_gate = a->variant != GDR_DELTANET;
@@ -208,8 +211,52 @@ int gdr_recurrent_commit(const gdr_args* a, const float* updates, const int32_t*
   if ((reinterpret_cast<uintptr_t>(a->h0) | reinterpret_cast<uintptr_t>(a->ht) |
        reinterpret_cast<uintptr_t>(updates)) % 16 != 0)
     return fail(GDR_ERR_INVALID, "initial/final state and updates must be 16-byte aligned");
+  return GDR_OK;
+}
+
+// Byte ranges [p, p + n) and [q, q + m) overlap.
+bool overlaps(const void* p, size_t n, const void* q, size_t m) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
+  return n && m && a < b + m && b < a + n;
+}
+
+}  // namespace
+
+int gdr_recurrent_commit(const gdr_args* a, const float* updates, const int32_t* accepted, hipStream_t stream) {
+  int rc = check_commit(a, updates);
+  if (rc) return rc;
   hipError_t e = gdr::launch_commit(*a, updates, accepted, stream);
   if (e != hipSuccess) return fail(GDR_ERR_HIP, "commit launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
+int gdr_recurrent_commit_verify(const gdr_args* prev, const float* prev_updates, const int32_t* accepted,
+                                const gdr_args* a, float* updates, hipStream_t stream) {
+  int rc = check_commit(prev, prev_updates);
+  if (rc) return rc;
+  if ((rc = check_common(a, false))) return rc;
+  if (a->q.dtype != a->k.dtype || a->q.dtype != a->v.dtype || a->q.dtype == GDR_F16)
+    return fail(GDR_ERR_UNSUPPORTED, "recurrent mode reads q, k, v of one dtype, bf16 or f32 (got dtype codes %d, %d, %d)",
+                a->q.dtype, a->k.dtype, a->v.dtype);
+  if (prev->variant != a->variant || prev->batch != a->batch || prev->heads != a->heads ||
+      prev->key_dim != a->key_dim || prev->value_dim != a->value_dim)
+    return fail(GDR_ERR_INVALID, "the previous block and the new block differ in variant or sizes");
+  if (prev->k.dtype != a->q.dtype)
+    return fail(GDR_ERR_UNSUPPORTED, "the previous block's key dtype (%d) differs from the new block's (%d)",
+                prev->k.dtype, a->q.dtype);
+  if (a->h0 != prev->ht)
+    return fail(GDR_ERR_INVALID, "the new block's initial state must be the committed state (args->h0 == prev->ht)");
+  if (!updates) return fail(GDR_ERR_INVALID, "updates: null pointer");
+  if (reinterpret_cast<uintptr_t>(updates) % 16) return fail(GDR_ERR_INVALID, "updates must be 16-byte aligned");
+  const size_t rows = size_t(a->batch) * a->heads * a->value_dim * sizeof(float);
+  const size_t state = size_t(a->batch) * a->heads * a->key_dim * a->value_dim * sizeof(float);
+  if (overlaps(updates, rows * a->seq_len, prev_updates, rows * prev->seq_len))
+    return fail(GDR_ERR_INVALID, "updates must not overlap the previous block's record");
+  if (a->ht && overlaps(a->ht, state, prev->ht, state))
+    return fail(GDR_ERR_INVALID, "the final state must not overlap the committed state");
+  hipError_t e = gdr::launch_commit_verify(*prev, prev_updates, accepted, *a, updates, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "commit-verify launch failed: %s", hipGetErrorString(e));
   g_last_error.clear();
   return GDR_OK;
 }

@@ -17,6 +17,11 @@ hipError_t launch_verify(const gdr_args& a, float* updates, hipStream_t stream);
 // a.h0, k, the gate and a verify record.
 hipError_t launch_commit(const gdr_args& a, const float* updates, const int32_t* accepted, hipStream_t stream);
 
+// launch_commit(prev, prev_updates, accepted) into prev.ht, then launch_verify(a, updates) from that state, in one
+// launch; a.h0 == prev.ht.
+hipError_t launch_commit_verify(const gdr_args& prev, const float* prev_updates, const int32_t* accepted,
+                                const gdr_args& a, float* updates, hipStream_t stream);
+
 // Enqueue the chunkwise forward; `a` has been validated (q, k, v share one dtype).
 hipError_t launch_chunk(const gdr_args& a, hipStream_t stream);
 

@@ -54,9 +54,15 @@ __device__ __forceinline__ float half_swap_sum(float x) {
 
 // q, k and v share one element type InT (bf16 or fp32; the host widens mixed or fp16 inputs to fp32, exactly), so
 // every load has a static type and the compiler can track each one's completion precisely.
-// The body of the decode kernel and of the verify kernel (kRecord: also store each token's update row).
-template <int VARIANT, int K, int VS, int kThreads, typename InT, bool kH0, bool kRecord>
-__device__ __forceinline__ void recurrent_body(const gdr_args& a, int n_slices, float* updates) {
+// The body of the decode kernel and of the verify kernel (kRecord: also store each token's update row).  With
+// kCommit it first applies the accepted prefix of the previous verified block (`c`: its k, gate, length, initial
+// state h0 and committed-state output ht; `prev_updates`: its update record) to the register-resident state, exactly
+// as the commit kernel does, writes that committed state to c.ht, and then verifies the new block from it; kH0 then
+// means c.h0 is non-null.
+template <int VARIANT, int K, int VS, int kThreads, typename InT, bool kH0, bool kRecord, bool kCommit = false>
+__device__ __forceinline__ void recurrent_body(const gdr_args& a, int n_slices, float* updates,
+                                               const gdr_args* c = nullptr, const float* prev_updates = nullptr,
+                                               const int32_t* accepted = nullptr) {
   constexpr int kWaves = kThreads / kWave;
   constexpr int NQ = VS / 4;           // float4 column quads per state row slice
   constexpr int RG = kThreads / NQ;    // row groups
@@ -85,7 +91,7 @@ __device__ __forceinline__ void recurrent_body(const gdr_args& a, int n_slices, 
   // q, k and the decay factors are stored row-group-major: channel r at position (r % RG) * RPT + r / RG, so a
   // thread's RPT rows rg, rg + RG, ... are contiguous and arrive in one or two wide LDS reads.
   __shared__ __align__(16) float s_q[kGroup][K], s_k[kGroup][K], s_eg[kGroup][kChannelGate ? K : 1];
-  __shared__ float s_v[kGroup][VS];
+  __shared__ __align__(16) float s_v[kGroup][VS];  // v rows; the previous block's update rows in the commit phase
   __shared__ float s_scalar[kGroup][2];  // beta, scalar decay
   __shared__ float s_qk[kGroup];         // q . k per token
   __shared__ __align__(16) float s_red[kWaves][2][VS];  // per-wave partial k S and q S
@@ -154,14 +160,65 @@ __device__ __forceinline__ void recurrent_body(const gdr_args& a, int n_slices, 
     }
   };
 
-  // The first group's vectors are requested before the state stream and staged in straight-line code, so staging
-  // waits for them alone while the state loads stay in flight.
-  if (T > 0) fetch(0);
   float4 st[RPT];  // (kH0 is a template argument: a run-time branch here would make the wait below conservative)
+  if constexpr (kCommit) {
+    // The previous block's accepted prefix, staged kGroup tokens at a time through the same LDS tiles (k and the
+    // decay factors row-group-major, the update rows in s_v): per token S <- decay_t S; S <- S + k_t^T u_t, with the
+    // commit kernel's operations in its order, so the committed state is bit-identical to gdr_recurrent_commit's.
+    const int Tc = c->seq_len;
+    const int n = accepted ? min(max(accepted[b], 0), Tc) : Tc;  // uniform over the workgroup
+    const InT* ckp = static_cast<const InT*>(c->k.ptr);
+    const float* cgp = static_cast<const float*>(c->gate.ptr);
+    const int64_t ckb = b * c->k.stride_b + h * c->k.stride_h;
+    const int64_t cgb = b * c->gate.stride_b + h * c->gate.stride_h;
+    const float* up = prev_updates + size_t(bh) * Tc * V + v0;
 #pragma unroll
-  for (int i = 0; i < RPT; ++i)
-    st[i] = kH0 ? load_stream4(h0 + lane_off + uint32_t(RG * i) * V) : make_float4(0.f, 0.f, 0.f, 0.f);
-  if (T > 0) stage(0);
+    for (int i = 0; i < RPT; ++i)
+      st[i] = kH0 ? load_stream4(c->h0 + state_base + lane_off + uint32_t(RG * i) * V) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int t0 = 0; t0 < n; t0 += kGroup) {
+      const int cnt = min(kGroup, n - t0);
+      if (t0 > 0) __syncthreads();  // the previous group's LDS reads are done
+      for (int i = tid; i < cnt * K; i += kThreads) {
+        const int tt = i / K, ch = i % K, pos = (ch % RG) * RPT + ch / RG;
+        s_k[tt][pos] = static_cast<float>(ckp[ckb + (t0 + tt) * c->k.stride_t + ch]);
+        if constexpr (kChannelGate) s_eg[tt][pos] = exp_fast(cgp[cgb + (t0 + tt) * c->gate.stride_t + ch]);
+      }
+      if constexpr (kScalarGate) {
+        if (tid < cnt) s_scalar[tid][1] = exp_fast(cgp[cgb + (t0 + tid) * c->gate.stride_t]);
+      }
+      for (int i = tid; i < cnt * NQ; i += kThreads) {
+        const int tt = i / NQ, qd = i % NQ;
+        *reinterpret_cast<float4*>(&s_v[tt][4 * qd]) =
+            *reinterpret_cast<const float4*>(up + size_t(t0 + tt) * V + 4 * qd);
+      }
+      __syncthreads();
+      for (int tt = 0; tt < cnt; ++tt) {
+        const float4 u = *reinterpret_cast<const float4*>(&s_v[tt][4 * quad]);
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+          if constexpr (kChannelGate) decay4(st[i], s_eg[tt][rg * RPT + i]);
+          if constexpr (kScalarGate) decay4(st[i], s_scalar[tt][1]);
+          rank1_update(st[i], s_k[tt][rg * RPT + i], u.x, u.y, u.z, u.w);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)  // each element is read and written by this thread only, so c.ht may be c.h0
+      *reinterpret_cast<float4*>(c->ht + state_base + lane_off + uint32_t(RG * i) * V) = st[i];
+    __syncthreads();  // the commit's LDS reads are done before the block is staged
+    if (T > 0) {
+      fetch(0);
+      stage(0);
+    }
+  } else {
+    // The first group's vectors are requested before the state stream and staged in straight-line code, so staging
+    // waits for them alone while the state loads stay in flight.
+    if (T > 0) fetch(0);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      st[i] = kH0 ? load_stream4(h0 + lane_off + uint32_t(RG * i) * V) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (T > 0) stage(0);
+  }
 
   // Per token: every wave folds its rows into per-wave partial sums of k S and q S (registers, then LDS); after a
   // barrier one thread per column adds the waves' partials in wave order, forms u and the output; after a second
@@ -268,6 +325,15 @@ __global__ __launch_bounds__(kThreads, 4) void recurrent_verify_kernel(const gdr
   recurrent_body<VARIANT, K, VS, kThreads, InT, kH0, true>(a, n_slices, updates);
 }
 
+// Commit of the previous block, then verify of the next, in one pass over the state (kH0: c.h0 is non-null).
+template <int VARIANT, int K, int VS, int kThreads, typename InT, bool kH0>
+__global__ __launch_bounds__(kThreads, 4) void recurrent_commit_verify_kernel(const gdr_args a, int n_slices,
+                                                                              float* updates, const gdr_args c,
+                                                                              const float* prev_updates,
+                                                                              const int32_t* accepted) {
+  recurrent_body<VARIANT, K, VS, kThreads, InT, kH0, true, true>(a, n_slices, updates, &c, prev_updates, accepted);
+}
+
 // State after the first n_b = clamp(accepted[b], 0, T) tokens of a verified block (all T when `accepted` is NULL):
 //   S = h0;  for t < n_b:  S <- decay_t S;  S <- S + k_t^T u_t      (u_t from the verify kernel's record)
 // Same workgroup tiling as the recurrent kernel (one [K, VS] column slice per workgroup, float4 column quads held in
@@ -342,19 +408,23 @@ __global__ __launch_bounds__(kThreads) void recurrent_commit_kernel(const gdr_ar
 }
 
 // Launch modes of the recurrent family: the forward, the verify forward (with the update record) and the commit.
-enum class RecMode { kForward, kVerify, kCommit };
+enum class RecMode { kForward, kVerify, kCommit, kCommitVerify };
 
 struct RecExtra {
-  float* record;             // kVerify: written
-  const float* updates;      // kCommit: read
-  const int32_t* accepted;   // kCommit: device [B] or NULL
+  float* record;             // kVerify, kCommitVerify: written
+  const float* updates;      // kCommit, kCommitVerify: read (the previous block's record)
+  const int32_t* accepted;   // kCommit, kCommitVerify: device [B] or NULL
+  const gdr_args* prev;      // kCommitVerify: the previous block's commit arguments
 };
 
 template <int VARIANT, int K, int VS, int kThreads, typename InT, bool kH0>
 static void launch_shape(const gdr_args& a, hipStream_t stream, RecMode mode, const RecExtra& x) {
   const int n_slices = a.value_dim / VS;
   const dim3 grid(a.batch * a.heads * n_slices), block(kThreads);
-  if (mode == RecMode::kCommit)
+  if (mode == RecMode::kCommitVerify)
+    hipLaunchKernelGGL((recurrent_commit_verify_kernel<VARIANT, K, VS, kThreads, InT, kH0>), grid, block, 0, stream,
+                       a, n_slices, x.record, *x.prev, x.updates, x.accepted);
+  else if (mode == RecMode::kCommit)
     hipLaunchKernelGGL((recurrent_commit_kernel<VARIANT, K, VS, kThreads, InT, kH0>), grid, block, 0, stream, a,
                        n_slices, x.updates, x.accepted);
   else if (mode == RecMode::kVerify)
@@ -376,7 +446,7 @@ static hipError_t launch_recurrent_k(const gdr_args& a, hipStream_t stream, int 
 
 template <int VARIANT, typename InT>
 static hipError_t launch_recurrent_v(const gdr_args& a, hipStream_t stream, int vs, RecMode mode, const RecExtra& x) {
-  if (a.h0)
+  if (mode == RecMode::kCommitVerify ? x.prev->h0 != nullptr : a.h0 != nullptr)
     return a.key_dim == 64 ? launch_recurrent_k<VARIANT, 64, InT, true>(a, stream, vs, mode, x)
                            : launch_recurrent_k<VARIANT, 128, InT, true>(a, stream, vs, mode, x);
   return a.key_dim == 64 ? launch_recurrent_k<VARIANT, 64, InT, false>(a, stream, vs, mode, x)
@@ -407,11 +477,17 @@ hipError_t launch_recurrent(const gdr_args& a, hipStream_t stream) {
 }
 
 hipError_t launch_verify(const gdr_args& a, float* updates, hipStream_t stream) {
-  return launch_family(a, stream, RecMode::kVerify, RecExtra{updates, nullptr, nullptr}, a.q.dtype);
+  return launch_family(a, stream, RecMode::kVerify, RecExtra{updates, nullptr, nullptr, nullptr}, a.q.dtype);
 }
 
 hipError_t launch_commit(const gdr_args& a, const float* updates, const int32_t* accepted, hipStream_t stream) {
-  return launch_family(a, stream, RecMode::kCommit, RecExtra{nullptr, updates, accepted}, a.k.dtype);
+  return launch_family(a, stream, RecMode::kCommit, RecExtra{nullptr, updates, accepted, nullptr}, a.k.dtype);
+}
+
+hipError_t launch_commit_verify(const gdr_args& prev, const float* prev_updates, const int32_t* accepted,
+                                const gdr_args& a, float* updates, hipStream_t stream) {
+  return launch_family(a, stream, RecMode::kCommitVerify, RecExtra{updates, prev_updates, accepted, &prev},
+                       a.q.dtype);
 }
 
 }  // namespace gdr

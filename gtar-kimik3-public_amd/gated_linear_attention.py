@@ -51,7 +51,13 @@ def verify_gated_linear_attention(
     scale: float | None = None,
     initial_state: torch.Tensor | None = None,
     output_final_state: bool = False,
+    pending=None,
+    accepted=None,
+    committed_out: torch.Tensor | None = None,
 ):
     """Speculative-decoding verify over a block of tokens: the recurrent forward plus a `VerifiedBlock` whose
-    `commit(accepted)` rebuilds the state after any accepted prefix.  Returns `(out, final_state or None, block)`."""
-    return verify(_lib.GLA, query, key, value, gate, None, scale, initial_state, output_final_state)
+    `commit(accepted)` rebuilds the state after any accepted prefix.  Returns `(out, final_state or None, block)`.
+    With `pending` (the previous block) the state is `pending.commit(accepted)`, computed in the same launch and
+    returned as the new block's `initial_state`; `initial_state` must then be None."""
+    return verify(_lib.GLA, query, key, value, gate, None, scale, initial_state, output_final_state, pending,
+                  accepted, committed_out)

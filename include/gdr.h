@@ -192,6 +192,17 @@ int gdr_recurrent_verify(const gdr_args* args, float* updates, hipStream_t strea
  * (src/cache.py:59-86, src/speculative.py:397, 425-449). */
 int gdr_recurrent_commit(const gdr_args* args, const float* updates, const int32_t* accepted, hipStream_t stream);
 
+/* One speculative cycle in one pass over the state: gdr_recurrent_commit(prev, prev_updates, accepted), which writes
+ * the committed state to prev->ht (may alias prev->h0), then gdr_recurrent_verify(args, updates) from that state,
+ * which must be args->h0 (== prev->ht).  Bit-identical to the two calls in sequence; the state is read once and
+ * held in registers for both, so a cycle streams it once each way instead of twice in and once out.  The previous
+ * block (k, gate, record, length) may differ from the new one in T only; its k has the new block's q/k/v dtype.
+ * `updates` must not overlap `prev_updates`, and args->ht (optional) must not overlap prev->ht.  Replaces the
+ * accept step of the previous cycle together with the verify forward of the next (src/speculative.py:351-356,
+ * 397, 425-449; src/cache.py:59-86). */
+int gdr_recurrent_commit_verify(const gdr_args* prev, const float* prev_updates, const int32_t* accepted,
+                                const gdr_args* args, float* updates, hipStream_t stream);
+
 /* Causal softmax attention of the hybrid stack's attention layer (grouped-query; forward only). */
 typedef struct gdr_attention_args {
   int32_t abi_version;       /* must equal GDR_ABI_VERSION */

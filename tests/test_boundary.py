@@ -167,6 +167,49 @@ def test_verify_and_commit_reject_bad_arguments_without_a_gpu():
     assert b"aligned" in so.gdr_last_error()
 
 
+def test_commit_verify_rejects_bad_arguments_without_a_gpu():
+    """gdr_recurrent_commit_verify: the commit's checks, the verify's checks, and the pairing rules (same variant and
+    sizes, one key dtype, args->h0 == prev->ht, no overlap of the records or of the two states).  Every call below
+    stops in validation, before any launch."""
+    so = lib.load_library()
+
+    def view(t, ptr, dtype, stride_t):
+        t.ptr, t.dtype, t.stride_t, t.stride_h, t.stride_b = ptr, dtype, stride_t, stride_t * 8, stride_t * 16
+
+    prev, a = lib.GdrArgs(), lib.GdrArgs()
+    for x in (prev, a):
+        x.abi_version = lib.ABI_VERSION
+        x.variant, x.batch, x.heads, x.seq_len, x.key_dim, x.value_dim = 0, 2, 2, 8, 64, 64
+        view(x.k, 1 << 20, lib.BF16, 64)
+        view(x.gate, 2 << 20, lib.F32, 64)
+    prev.ht = 3 << 20
+    for name, ptr in (("q", 4 << 20), ("v", 5 << 20), ("out", 6 << 20)):
+        view(getattr(a, name), ptr, lib.BF16, 64)
+    view(a.beta, 7 << 20, lib.F32, 1)
+    a.h0 = prev.ht
+    rec = 8 << 20  # the previous record: 2 * 2 * 8 * 64 * 4 = 8 KiB
+
+    call = lambda upd, new_upd: so.gdr_recurrent_commit_verify(ctypes.byref(prev), upd, None, ctypes.byref(a),
+                                                               new_upd, None)
+    assert call(None, rec + (1 << 16)) == -1 and b"updates" in so.gdr_last_error()
+    assert call(rec, None) == -1 and b"updates" in so.gdr_last_error()
+    assert call(rec, rec + 4096) == -1 and b"overlap" in so.gdr_last_error()
+    a.ht = prev.ht + 1024
+    assert call(rec, rec + (1 << 16)) == -1 and b"overlap" in so.gdr_last_error()
+    a.ht = 0
+    a.h0 = prev.ht + 4096
+    assert call(rec, rec + (1 << 16)) == -1 and b"committed state" in so.gdr_last_error()
+    a.h0 = prev.ht
+    prev.heads = 4
+    assert call(rec, rec + (1 << 16)) == -1 and b"differ" in so.gdr_last_error()
+    prev.heads = 2
+    prev.k.dtype = lib.F32
+    assert call(rec, rec + (1 << 16)) == -2 and b"dtype" in so.gdr_last_error()
+    prev.k.dtype = lib.BF16
+    prev.ht = 0
+    assert call(rec, rec + (1 << 16)) == -1 and b"ht" in so.gdr_last_error()
+
+
 class _FakeBlock:
     """Stands in for a VerifiedBlock on the CPU: commit(n) returns a recognisable state."""
 

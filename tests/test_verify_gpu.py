@@ -5,7 +5,8 @@ state relative Frobenius error <= 1e-2), and bit for bit against the recurrent o
 the record store).  The committed state after n accepted tokens against the recurrence over the first n tokens
 (same tolerance), and bit for bit against the recurrent op run on those n tokens alone, which is the op-level form
 of the reference's fork -> verify -> rollback -> replay equivalence (tests/test_speculative.py:844-893) and of its
-full-accept commit equivalence (:896-936).
+full-accept commit equivalence (:896-936).  The one-launch cycle (gdr_recurrent_commit_verify) bit for bit against
+commit followed by verify.
 """
 
 import pytest
@@ -161,3 +162,64 @@ def test_cache_fork_verify_accept_equals_clean_run():
         with torch.no_grad():
             _, clean = gdr.recurrent_kimi_delta_attention(*part.args(), initial_state=saved, output_final_state=True)
         assert torch.equal(cache.state, clean)
+
+
+def _accept_counts(B, T):
+    """Per-sequence accept counts on the device covering 0, T and values in between."""
+    counts = [(3 * i) % (T + 1) for i in range(B)]
+    counts[0], counts[-1] = 0, T
+    return torch.tensor(counts, dtype=torch.int32, device="cuda")
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+@pytest.mark.parametrize("shape", [(2, 4, 8, 5, 128, 128), (3, 2, 3, 8, 64, 64), (64, 16, 8, 8, 128, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_commit_verify_equals_commit_then_verify(variant, shape, dtype):
+    """One launch per cycle against the two-launch cycle: out, the new record, the committed state and the final
+    state bit for bit, with per-sequence accept counts on the device, a previous block of another length, and a
+    previous block that started from a zero state."""
+    B, H, Tp, T, K, V = shape
+    fn = VERIFY_FNS[variant]
+    acc = _accept_counts(B, Tp)
+    for state_std in (0.5, None):
+        print(f"commit-verify {variant} {dtype} B={B} H={H} Tp={Tp} T={T} K={K} V={V} h0={state_std}", flush=True)
+        prev = workloads.make_inputs(variant, B, Tp, H, K, V, seed=21, dtype=dtype, state_std=state_std,
+                                     device="cuda")
+        nxt = workloads.make_inputs(variant, B, T, H, K, V, seed=22, dtype=dtype, device="cuda")
+        with torch.no_grad():
+            _, _, block = fn(*prev.args(), initial_state=prev.initial_state)
+            committed = block.commit(acc)
+            out_ref, final_ref, block_ref = fn(*nxt.args(), initial_state=committed, output_final_state=True)
+            out, final, new_block = fn(*nxt.args(), output_final_state=True, pending=block, accepted=acc)
+        assert torch.equal(new_block.initial_state, committed)
+        assert torch.equal(out, out_ref) and torch.equal(final, final_ref)
+        assert torch.equal(new_block.updates, block_ref.updates)
+
+
+def test_commit_verify_chain_in_place():
+    """Three cycles, each committing over the previous block's initial state in place, with int, None (all tokens)
+    and zero accept counts, against the two-launch cycle; then a cycle whose blocks differ in dtype, which takes the
+    two-launch path."""
+    B, H, T, K, V = 4, 4, 6, 128, 128
+    inputs = [workloads.make_inputs("kda", B, T, H, K, V, seed=30 + i, device="cuda") for i in range(4)]
+    state0 = torch.randn(B, H, K, V, device="cuda") * 0.3
+    fn = gdr.verify_kimi_delta_attention
+    counts = (3, None, 0)
+    with torch.no_grad():
+        ref = []
+        _, _, blk = fn(*inputs[0].args(), initial_state=state0.clone())
+        for inp, n in zip(inputs[1:], counts):
+            s = blk.commit(n)
+            o, _, blk = fn(*inp.args(), initial_state=s)
+            ref.append((o, s))
+        s = state0.clone()
+        _, _, blk = fn(*inputs[0].args(), initial_state=s)
+        for (o_ref, s_ref), inp, n in zip(ref, inputs[1:], counts):
+            print(f"in-place cycle accepted={n}", flush=True)
+            o, _, blk = fn(*inp.args(), pending=blk, accepted=n, committed_out=blk.initial_state)
+            assert blk.initial_state.data_ptr() == s.data_ptr()
+            assert torch.equal(o, o_ref) and torch.equal(blk.initial_state, s_ref)
+        f32 = workloads.make_inputs("kda", B, T, H, K, V, seed=40, dtype=torch.float32, device="cuda")
+        o_mixed, _, _ = fn(*f32.args(), pending=blk, accepted=2)
+        o_two, _, _ = fn(*f32.args(), initial_state=blk.commit(2))
+    assert torch.equal(o_mixed, o_two)
