@@ -172,26 +172,50 @@ __device__ __forceinline__ void recurrent_body(const gdr_args& a, int n_slices, 
     const int64_t ckb = b * c->k.stride_b + h * c->k.stride_h;
     const int64_t cgb = b * c->gate.stride_b + h * c->gate.stride_h;
     const float* up = prev_updates + size_t(bh) * Tc * V + v0;
+    // Its group registers use the verify's element-to-thread mapping (element i of a group to thread i % kThreads).
+    constexpr int NU = (kGroup * NQ + kThreads - 1) / kThreads;  // update-row quads per thread and group
+    InT ck[NK];
+    float cg[NK], csg = 0.f;
+    float4 cu[NU];
+    auto cfetch = [&](int t0, int cnt) {
 #pragma unroll
-    for (int i = 0; i < RPT; ++i)
-      st[i] = kH0 ? load_stream4(c->h0 + state_base + lane_off + uint32_t(RG * i) * V) : make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int t0 = 0; t0 < n; t0 += kGroup) {
-      const int cnt = min(kGroup, n - t0);
-      if (t0 > 0) __syncthreads();  // the previous group's LDS reads are done
-      for (int i = tid; i < cnt * K; i += kThreads) {
-        const int tt = i / K, ch = i % K, pos = (ch % RG) * RPT + ch / RG;
-        s_k[tt][pos] = static_cast<float>(ckp[ckb + (t0 + tt) * c->k.stride_t + ch]);
-        if constexpr (kChannelGate) s_eg[tt][pos] = exp_fast(cgp[cgb + (t0 + tt) * c->gate.stride_t + ch]);
+      for (int j = 0; j < NK; ++j) {
+        const int i = tid + j * kThreads, tt = i / K, ch = i % K;
+        if (i < kGroup * K && tt < cnt) {
+          ck[j] = ckp[ckb + (t0 + tt) * c->k.stride_t + ch];
+          if constexpr (kChannelGate) cg[j] = cgp[cgb + (t0 + tt) * c->gate.stride_t + ch];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NU; ++j) {
+        const int i = tid + j * kThreads, tt = i / NQ, qd = i % NQ;
+        if (i < kGroup * NQ && tt < cnt) cu[j] = *reinterpret_cast<const float4*>(up + size_t(t0 + tt) * V + 4 * qd);
       }
       if constexpr (kScalarGate) {
-        if (tid < cnt) s_scalar[tid][1] = exp_fast(cgp[cgb + (t0 + tid) * c->gate.stride_t]);
+        if (tid < cnt) csg = cgp[cgb + (t0 + tid) * c->gate.stride_t];
       }
-      for (int i = tid; i < cnt * NQ; i += kThreads) {
-        const int tt = i / NQ, qd = i % NQ;
-        *reinterpret_cast<float4*>(&s_v[tt][4 * qd]) =
-            *reinterpret_cast<const float4*>(up + size_t(t0 + tt) * V + 4 * qd);
+    };
+    auto cstage = [&](int cnt) {
+#pragma unroll
+      for (int j = 0; j < NK; ++j) {
+        const int i = tid + j * kThreads, tt = i / K, ch = i % K, pos = (ch % RG) * RPT + ch / RG;
+        if (i < kGroup * K && tt < cnt) {
+          s_k[tt][pos] = static_cast<float>(ck[j]);
+          if constexpr (kChannelGate) s_eg[tt][pos] = exp_fast(cg[j]);
+        }
       }
-      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < NU; ++j) {
+        const int i = tid + j * kThreads, tt = i / NQ, qd = i % NQ;
+        if (i < kGroup * NQ && tt < cnt) *reinterpret_cast<float4*>(&s_v[tt][4 * qd]) = cu[j];
+      }
+      if constexpr (kScalarGate) {
+        if (tid < cnt) s_scalar[tid][1] = exp_fast(csg);
+      }
+    };
+    // Request order: the first commit group, the state, then the block's first group, so each wait below covers
+    // only what it needs (loads complete in order) and the block's vectors arrive during the commit.
+    auto capply = [&](int cnt) {
       for (int tt = 0; tt < cnt; ++tt) {
         const float4 u = *reinterpret_cast<const float4*>(&s_v[tt][4 * quad]);
 #pragma unroll
@@ -201,15 +225,31 @@ __device__ __forceinline__ void recurrent_body(const gdr_args& a, int n_slices, 
           rank1_update(st[i], s_k[tt][rg * RPT + i], u.x, u.y, u.z, u.w);
         }
       }
+    };
+    // The first group is straight-line code (a group of 0 tokens loads and stages nothing), so the wait before its
+    // staging can count the later loads precisely; later groups (blocks longer than kGroup) loop.
+    const int cnt0 = min(kGroup, n);
+    cfetch(0, cnt0);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      st[i] = kH0 ? load_stream4(c->h0 + state_base + lane_off + uint32_t(RG * i) * V) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (T > 0) fetch(0);
+    cstage(cnt0);
+    __syncthreads();
+    capply(cnt0);
+    for (int t0 = kGroup; t0 < n; t0 += kGroup) {
+      const int cnt = min(kGroup, n - t0);
+      __syncthreads();  // the previous group's LDS reads are done
+      cfetch(t0, cnt);
+      cstage(cnt);
+      __syncthreads();
+      capply(cnt);
     }
 #pragma unroll
     for (int i = 0; i < RPT; ++i)  // each element is read and written by this thread only, so c.ht may be c.h0
       *reinterpret_cast<float4*>(c->ht + state_base + lane_off + uint32_t(RG * i) * V) = st[i];
     __syncthreads();  // the commit's LDS reads are done before the block is staged
-    if (T > 0) {
-      fetch(0);
-      stage(0);
-    }
+    if (T > 0) stage(0);
   } else {
     // The first group's vectors are requested before the state stream and staged in straight-line code, so staging
     // waits for them alone while the state loads stay in flight.
