@@ -51,7 +51,9 @@ def short_convolution(
         x = x.contiguous()
     out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
     state_in = conv_state.to(x.dtype).contiguous() if conv_state is not None else None
-    state_out = torch.empty_like(state_in) if state_in is not None else None
+    # The kernel writes the new state of every sequence that has tokens; a sequence of length 0 (and every sequence
+    # when T == 0, which launches nothing) keeps its state, as the reference's does.
+    state_out = state_in.clone() if state_in is not None else None
     _lib.short_conv(x, out, w, state_in, state_out, cu_seqlens, activation, x.device)
     if conv_state is not None:
         conv_state.copy_(state_out)

@@ -232,13 +232,8 @@ __global__ __launch_bounds__(kAttnThreads, 4) void attention_fwd_kernel(const gd
 template <int D, typename T>
 hipError_t launch_attention_typed(const gdr_attention_args& a, hipStream_t stream) {
   constexpr int lds = 4 * kBN * D * 2;  // K and V, double-buffered
-  static bool configured = false;       // benign race: every thread sets the same attribute
-  if (!configured) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_fwd_kernel<D, T>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  const hipError_t e = configure_lds<&attention_fwd_kernel<D, T>>(lds);
+  if (e != hipSuccess) return e;
   const int nqb = (a.seq_len + kBM - 1) / kBM;
   const int64_t slots = a.cu_seqlens ? int64_t(nqb) + a.n_seqs : int64_t(a.batch) * nqb;
   if (slots * a.heads > 0)

@@ -596,13 +596,8 @@ hipError_t launch_typed(const gdr_args& a, hipStream_t stream) {
   const int n_slices = a.value_dim / kSlice;
   const int xcd_map = (bh % 8 == 0) ? 1 : 0;
   constexpr int bytes = Lds<K>::BYTES;
-  static bool configured = false;  // benign race: every thread sets the same attribute
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_fwd_kernel<VARIANT, K, OutT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  const hipError_t e = configure_lds<&chunk_fwd_kernel<VARIANT, K, OutT>>(bytes);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((chunk_fwd_kernel<VARIANT, K, OutT>), dim3(bh * n_slices), dim3(512), bytes, stream, a,
                      n_slices, xcd_map);
   return hipGetLastError();

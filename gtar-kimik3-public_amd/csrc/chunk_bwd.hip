@@ -1102,19 +1102,10 @@ hipError_t launch_bwd_typed(const gdr_args& a, const gdr_grads& g, const BwdLayo
   const int64_t rec = Rec<K>::bytes(a.value_dim);
   constexpr int dscan_lds = 2 * (Rec<K>::FIX + kChunk * kScanSlice * 2);
   constexpr int grad_lds = GradLds<K>::BYTES;
-  static bool configured = false;  // benign race: every thread sets the same attributes
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_dscan_kernel<VARIANT, K>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, dscan_lds);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_grad_kernel<VARIANT, K>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, grad_lds);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_sprod_kernel<VARIANT, K>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, SprodLds<K>::BYTES);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  hipError_t e = configure_lds<&chunk_dscan_kernel<VARIANT, K>>(dscan_lds);
+  if (e == hipSuccess) e = configure_lds<&chunk_grad_kernel<VARIANT, K>>(grad_lds);
+  if (e == hipSuccess) e = configure_lds<&chunk_sprod_kernel<VARIANT, K>>(SprodLds<K>::BYTES);
+  if (e != hipSuccess) return e;
   if (nc == 0) return hipSuccess;
   float* states = reinterpret_cast<float*>(ws + Lw.states);
   float* dstates = reinterpret_cast<float*>(ws + Lw.dstates);

@@ -1009,17 +1009,6 @@ int64_t slots_per_head(const gdr_args& a) {
   return int64_t(a.batch) * ((a.seq_len + kChunk - 1) / kChunk);
 }
 
-// Sets a kernel's dynamic-LDS limit once per instantiation (a benign race: every thread sets the same value).
-template <auto Kernel>
-hipError_t configure_lds(int bytes) {
-  static bool done = false;
-  if (done) return hipSuccess;
-  const hipError_t e =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  if (e == hipSuccess) done = true;
-  return e;
-}
-
 template <int VARIANT, int K, int kPro>
 hipError_t launch_prep(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
   const int nc = (a.seq_len + kChunk - 1) / kChunk;

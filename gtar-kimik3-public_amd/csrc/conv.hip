@@ -69,11 +69,12 @@ __global__ __launch_bounds__(256) void short_conv_kernel(const gdr_conv_args a, 
   for (int k = 0; k < kConvTok; ++k) {
     const int t = t0 + k;
     if (t >= a.seq_len) break;
-    while (t >= end) {  // the next packed sequence starts inside this thread's tokens
+    while (t >= end && n + 1 < a.n_seqs) {  // the next packed sequence starts inside this thread's tokens
       ++n;
       bos = end;
       end = a.cu_seqlens[n + 1];
     }
+    if (t >= end) break;  // past cu_seqlens[n_seqs] (a caller that breaks the offsets contract): nothing to do
     const size_t state_row = size_t(n) * C;  // [N, C, W - 1]
     float acc[VEC];
 #pragma unroll

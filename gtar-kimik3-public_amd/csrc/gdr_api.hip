@@ -298,6 +298,10 @@ int gdr_short_conv_fwd(const gdr_conv_args* a, hipStream_t stream) {
     return fail(GDR_ERR_UNSUPPORTED, "kernel size %d not supported (2 to 8)", a->kernel_size);
   if (a->cu_seqlens && (a->batch != 1 || a->n_seqs < 1))
     return fail(GDR_ERR_INVALID, "cu_seqlens requires batch == 1 and n_seqs >= 1");
+  if (a->seq_len == 0) {  // no token: nothing to compute and no state entry to write (x, out may be NULL)
+    g_last_error.clear();
+    return GDR_OK;
+  }
   int rc;
   if ((rc = check_view(a->x, "x", true, false)) || (rc = check_view(a->out, "out", true, false))) return rc;
   if (a->out.dtype != a->x.dtype) return fail(GDR_ERR_UNSUPPORTED, "out must have x's dtype");

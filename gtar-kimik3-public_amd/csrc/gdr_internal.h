@@ -7,6 +7,16 @@
 
 namespace gdr {
 
+// Raises a kernel's dynamic-LDS limit to `bytes` once per process.  The function-local static is initialised by
+// exactly one thread (C++11 guarantees it), so concurrent first calls from several host threads are race-free; a
+// failure is remembered and returned by every later call.
+template <auto Kernel>
+hipError_t configure_lds(int bytes) {
+  static const hipError_t status = hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  return status;
+}
+
 // Enqueue the recurrent forward; `a` has been validated.
 hipError_t launch_recurrent(const gdr_args& a, hipStream_t stream);
 

@@ -69,7 +69,9 @@ typedef struct gdr_args {
   gdr_tensor out;      /* written; dtype bf16, f16 or f32 */
   const float* h0;     /* [N, H, K, V] f32 contiguous, or NULL for a zero initial state */
   float* ht;           /* [N, H, K, V] f32 contiguous, or NULL when the final state is not wanted */
-  const int32_t* cu_seqlens; /* device int32 [n_seqs + 1] packed-sequence offsets, or NULL */
+  const int32_t* cu_seqlens; /* device int32 [n_seqs + 1] packed-sequence offsets, or NULL: cu[0] = 0,
+                                non-decreasing, cu[n_seqs] = T (a sequence may be empty: its final state is its
+                                initial state) */
   int32_t n_seqs;            /* number of packed sequences (N); ignored when cu_seqlens is NULL (N = B) */
   int32_t reserved;
   void* workspace;           /* chunk mode: device scratch of gdr_chunk_workspace_bytes(args) bytes, 256-aligned;
@@ -240,12 +242,14 @@ typedef struct gdr_conv_args {
   const void* weight;        /* [C, W] in x's dtype: nn.Conv1d(C, C, W, groups=C).weight viewed as [C, W] */
   const void* state_in;      /* [N, C, W - 1] in x's dtype: the W - 1 inputs before each sequence, or NULL (zeros) */
   void* state_out;           /* [N, C, W - 1]: the last W - 1 inputs of each sequence after the call, or NULL; must
-                                not alias state_in */
-  const int32_t* cu_seqlens; /* device int32 [n_seqs + 1], or NULL (N = B) */
+                                not alias state_in.  The entry of a sequence of length 0 is not written (a caller
+                                that wants it unchanged copies state_in there first) */
+  const int32_t* cu_seqlens; /* device int32 [n_seqs + 1], or NULL (N = B): cu[0] = 0, non-decreasing,
+                                cu[n_seqs] = T; tokens past cu[n_seqs] are not computed */
 } gdr_conv_args;
 
 /* out[t, c] = act(sum_{j < W} weight[c, j] x[t - W + 1 + j, c]), where inputs before a sequence's first token come
- * from state_in (or are zero) -- never from the previous packed sequence.  Replaces ShortConvolution.forward
+ * from state_in (or are zero) -- never from the previous packed sequence.  T == 0 is a no-op (pointers unused).  Replaces ShortConvolution.forward
  * (src/layers/short_convolution.py:11-20), whose padded conv runs across the batch layout and has no notion of packed
  * sequences (:9, :15), including its conv-state path (:16-19). */
 int gdr_short_conv_fwd(const gdr_conv_args* args, hipStream_t stream);

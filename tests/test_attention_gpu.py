@@ -103,3 +103,38 @@ def test_short_convolution_batched_matches_reference_module():
     assert ((out.cpu().double() - ref).abs().max() / ref.abs().max()).item() <= 1e-2
     lin, _ = oracle.short_convolution(x, w, activation=False)
     assert ((plain.cpu().double() - lin).abs().max() / lin.abs().max()).item() <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_short_convolution_empty_sequences_keep_their_state(dtype):
+    """Packed sequences of length 0 (first, inner and last) keep their conv state, as in the oracle (the reference
+    leaves its cache untouched when no token arrives)."""
+    lens, C, W = [0, 3, 0, 70, 1, 0], 32, 4
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    T = int(cu[-1])
+    gen = torch.Generator().manual_seed(6)
+    x = torch.randn(1, T, C, generator=gen).to(dtype)
+    w = (torch.randn(C, 1, W, generator=gen) * 0.5).to(dtype)
+    state = torch.randn(len(lens), C, W - 1, generator=gen).to(dtype)
+    ref, ref_state = oracle.short_convolution(x, w, state, cu)
+    st = state.cuda()
+    with torch.no_grad():
+        out = gdr.short_convolution(x.cuda(), w.cuda(), st, cu_seqlens=cu.cuda())
+    assert ((out.cpu().double() - ref).abs().max() / ref.abs().max()).item() <= 1e-2
+    assert torch.equal(st.cpu(), ref_state.to(dtype))
+    for n, length in enumerate(lens):
+        if length == 0:
+            assert torch.equal(st[n].cpu(), state[n])
+
+
+def test_short_convolution_zero_tokens_keeps_the_state():
+    """T == 0 launches nothing; the state passed in comes back unchanged."""
+    gen = torch.Generator().manual_seed(7)
+    x = torch.zeros(2, 0, 64).bfloat16()
+    w = torch.randn(64, 1, 4, generator=gen).bfloat16()
+    state = torch.randn(2, 64, 3, generator=gen).bfloat16()
+    st = state.cuda()
+    with torch.no_grad():
+        out = gdr.short_convolution(x.cuda(), w.cuda(), st)
+    torch.cuda.synchronize()
+    assert out.shape == (2, 0, 64) and torch.equal(st.cpu(), state)

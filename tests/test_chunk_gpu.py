@@ -216,3 +216,41 @@ def test_chunk_varlen_packed_prefill_config():
     eo, es = out_error(out, ref_o), state_error(state, ref_s)
     print(f"varlen packed config: out err {eo:.2e} state err {es:.2e}", flush=True)
     assert eo <= OUT_TOL and es <= STATE_TOL
+
+
+def test_chunk_varlen_packed_prefill_config_sixteen_heads():
+    """The packed-prefill configuration at its stated shape: 32 sequences with lengths ~U[256, 4096] at H=16,
+    dk=dv=128, KDA, per-sequence initial states, against the oracle run sequence by sequence."""
+    lengths = workloads.varlen_lengths(32, 256, 4096, seed=0)
+    print(f"varlen KDA 32 seqs, {sum(lengths)} tokens, H=16", flush=True)
+    inp, cu = workloads.make_varlen_inputs("kda", lengths, 16, 128, 128, seed=0, device="cuda")
+    with torch.no_grad():
+        out, state = CHUNK_FNS["kda"](*inp.args(), initial_state=inp.initial_state, output_final_state=True,
+                                      cu_seqlens=cu)
+    torch.cuda.synchronize()
+    q, k, v, g, beta, h0 = oracle_args(inp)
+    ref_o, ref_s = oracle.varlen(oracle.chunkwise, "kda", q, k, v, g, beta, None, h0, cu.cpu())
+    eo, es = out_error(out, ref_o), state_error(state, ref_s)
+    print(f"varlen packed config H=16: out err {eo:.2e} state err {es:.2e}", flush=True)
+    assert eo <= OUT_TOL and es <= STATE_TOL
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_chunk_varlen_empty_sequences(variant):
+    """Packed sequences of length 0 (first, inner, last): each one's final state is its initial state, exactly; the
+    other sequences match the oracle."""
+    lens = [0, 100, 0, 64, 1, 0]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    H, K, V = 2, 128, 128
+    inp = workloads.make_inputs(variant, 1, int(cu[-1]), H, K, V, seed=21, device="cuda")
+    h0 = torch.randn(len(lens), H, K, V, generator=torch.Generator().manual_seed(22)) * 0.1
+    with torch.no_grad():
+        out, state = CHUNK_FNS[variant](*inp.args(), initial_state=h0.cuda(), output_final_state=True,
+                                        cu_seqlens=cu.cuda())
+    torch.cuda.synchronize()
+    for n, length in enumerate(lens):
+        if length == 0:
+            assert torch.equal(state[n].cpu(), h0[n]), n
+    q, k, v, g, beta, _ = oracle_args(inp)
+    ref_o, ref_s = oracle.varlen(oracle.chunkwise, variant, q, k, v, g, beta, None, h0, cu)
+    assert out_error(out, ref_o) <= OUT_TOL and state_error(state, ref_s) <= STATE_TOL

@@ -39,3 +39,32 @@ def test_stack_matches_oracle_on_packed_sequences():
         es = ((s.cpu().double() - r).norm() / r.norm()).item()
         print(f"  layer {i} state err {es:.2e}")
         assert es <= 3e-2
+
+
+def test_stack_full_shape_packed_equals_each_sequence_alone():
+    """The packed-prefill configuration at its stated shape (hidden 1024, 16 x 128 heads, 3 KDA + 1 attention
+    blocks, 32 sequences with lengths ~U[256, 4096]): the packed forward equals each sequence run on its own, to the
+    stack's bar on the residual update and on the KDA states (a property that holds at any size, so no fp64 oracle
+    has to run the full configuration)."""
+    workloads = importlib.import_module("gtar-kimik3-public_amd.workloads")
+    cfg = stack.StackConfig()
+    model = stack.HybridStack(cfg, stack.init_weights(cfg, seed=0))
+    lengths = workloads.varlen_lengths(32, 256, 4096, seed=0)
+    cu = torch.tensor([0] + torch.tensor(lengths).cumsum(0).tolist(), dtype=torch.int32)
+    T = int(cu[-1])
+    print(f"stack full shape: {len(lengths)} seqs, {T} tokens", flush=True)
+    hidden = torch.randn(1, T, cfg.hidden_size, generator=torch.Generator().manual_seed(1)).bfloat16().cuda()
+    out, states = model.forward(hidden, cu.cuda())
+    worst_out, worst_state = 0.0, 0.0
+    for n, length in enumerate(lengths):
+        a, b = int(cu[n]), int(cu[n + 1])
+        one, one_states = model.forward(hidden[:, a:b].contiguous(), torch.tensor([0, length], dtype=torch.int32,
+                                                                                    device="cuda"))
+        ref_delta = one[0].double() - hidden[0, a:b].double()
+        delta = out[0, a:b].double() - hidden[0, a:b].double()
+        worst_out = max(worst_out, ((delta - ref_delta).abs().max() / ref_delta.abs().max()).item())
+        for s, r in zip(states, one_states):
+            if r is not None:
+                worst_state = max(worst_state, ((s[n].double() - r[0].double()).norm() / r[0].double().norm()).item())
+    print(f"stack full shape: worst residual-update err {worst_out:.2e}, worst state err {worst_state:.2e}")
+    assert worst_out <= 5e-2 and worst_state <= 3e-2

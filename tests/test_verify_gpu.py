@@ -28,6 +28,7 @@ SHAPES = [
     (2, 4, 5, 128, 128),
     (3, 2, 8, 64, 64),
     (1, 2, 3, 128, 256),
+    (2, 4, 17, 128, 128),  # three 8-token staging groups, the last one partial
     (64, 16, 8, 128, 128),  # wide 128-column slices (B * H * V / 128 >= 1024 workgroups)
 ]
 
@@ -61,9 +62,10 @@ def test_verify_matches_oracle_and_recurrent(variant, shape):
 
 
 @pytest.mark.parametrize("variant", oracle.VARIANTS)
-def test_commit_every_prefix(variant):
-    B, H, T, K, V = 2, 3, 8, 128, 64
-    print(f"commit prefixes {variant}", flush=True)
+@pytest.mark.parametrize("T", [8, 17])  # 17: three groups of the 8-token staging, the last one partial
+def test_commit_every_prefix(variant, T):
+    B, H, K, V = 2, 3, 128, 64
+    print(f"commit prefixes {variant} T={T}", flush=True)
     inp = workloads.make_inputs(variant, B, T, H, K, V, seed=12, state_std=0.5, device="cuda")
     with torch.no_grad():
         _, _, block = VERIFY_FNS[variant](*inp.args(), initial_state=inp.initial_state)
@@ -172,7 +174,8 @@ def _accept_counts(B, T):
 
 
 @pytest.mark.parametrize("variant", oracle.VARIANTS)
-@pytest.mark.parametrize("shape", [(2, 4, 8, 5, 128, 128), (3, 2, 3, 8, 64, 64), (64, 16, 8, 8, 128, 128)])
+@pytest.mark.parametrize("shape", [(2, 4, 8, 5, 128, 128), (3, 2, 3, 8, 64, 64), (64, 16, 8, 8, 128, 128),
+                                   (2, 4, 17, 9, 128, 128), (3, 2, 9, 17, 64, 64)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_commit_verify_equals_commit_then_verify(variant, shape, dtype):
     """One launch per cycle against the two-launch cycle: out, the new record, the committed state and the final
