@@ -153,6 +153,7 @@ EXPORTS = {
     "gdr_chunk_bwd_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(GdrArgs)]),
     "gdr_chunk_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
     "gdr_chunk_fwd_fused": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.POINTER(GdrPrologue), ctypes.c_void_p]),
+    "gdr_chunk_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
     "gdr_chunk_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(GdrArgs)]),
     "gdr_recurrent_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
     "gdr_recurrent_verify": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p]),

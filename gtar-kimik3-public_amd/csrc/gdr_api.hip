@@ -3,9 +3,17 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+#include <mutex>
 #include <string>
 
 #include "gdr_internal.h"
+
+// Device scratch of gdr_chunk_fwd_noalloc: the chunk path's workspace for callers that cannot allocate.  Each GPU the
+// library runs on holds its own copy from the first such call until the process ends.  In host code `scratch`
+// names a host-side stand-in, never the device array: kernels get the per-device address that
+// hipGetSymbolAddress returns (scratch_on_device below).
+static __device__ __align__(256) unsigned char scratch[GDR_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -120,6 +128,34 @@ int check_prologue(const gdr_args* a, const gdr_prologue* pro) {
     return fail(GDR_ERR_INVALID, "gate_bias must be 16-byte aligned");
   if (!pro->a_log) return fail(GDR_ERR_INVALID, "a_log: null pointer");
   return GDR_OK;
+}
+
+// Address of `scratch` on `device`, looked up once per device (with that device current) and kept.
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+hipError_t scratch_on_device(int device, void** out) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  void* p = g_scratch_ptr[device].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[device].load(std::memory_order_relaxed);
+    if (!p) {
+      int current = -1;
+      hipError_t e = hipGetDevice(&current);
+      if (e != hipSuccess) return e;
+      if (current != device && (e = hipSetDevice(device)) != hipSuccess) return e;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      const hipError_t restore = current != device ? hipSetDevice(current) : hipSuccess;
+      if (e != hipSuccess) return e;
+      if (restore != hipSuccess) return restore;
+      if (!p) return hipErrorInvalidSymbol;
+      g_scratch_ptr[device].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return hipSuccess;
 }
 
 int chunk_fwd(const gdr_args* a, const gdr_prologue* pro, hipStream_t stream) {
@@ -365,6 +401,28 @@ int64_t gdr_chunk_workspace_bytes(const gdr_args* a) {
 }
 
 int gdr_chunk_fwd(const gdr_args* a, hipStream_t stream) { return chunk_fwd(a, nullptr, stream); }
+
+int gdr_chunk_fwd_noalloc(const gdr_args* a, hipStream_t stream) {
+  int rc = check_shape(a, true);
+  if (rc) return rc;
+  if (a->workspace) return fail(GDR_ERR_INVALID, "gdr_chunk_fwd_noalloc: workspace must be NULL (the library's "
+                                "device scratch is used)");
+  const int64_t need = gdr::chunk_workspace_bytes(*a);
+  if (need > GDR_NOALLOC_SCRATCH_BYTES)
+    return fail(GDR_ERR_UNSUPPORTED, "gdr_chunk_fwd_noalloc: this call needs %lld bytes of scratch, above the "
+                "library's fixed %lld (one record per 64-token chunk and head); use gdr_chunk_fwd with a workspace",
+                (long long)need, (long long)GDR_NOALLOC_SCRATCH_BYTES);
+  int device = -1;
+  hipError_t e = hipStreamGetDevice(stream, &device);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "gdr_chunk_fwd_noalloc: stream device: %s", hipGetErrorString(e));
+  void* ptr = nullptr;
+  if ((e = scratch_on_device(device, &ptr)) != hipSuccess)
+    return fail(GDR_ERR_HIP, "gdr_chunk_fwd_noalloc: scratch address on device %d: %s", device, hipGetErrorString(e));
+  gdr_args b = *a;
+  b.workspace = ptr;
+  b.workspace_bytes = GDR_NOALLOC_SCRATCH_BYTES;
+  return chunk_fwd(&b, nullptr, stream);
+}
 
 int gdr_chunk_fwd_fused(const gdr_args* a, const gdr_prologue* pro, hipStream_t stream) {
   if (!pro) return fail(GDR_ERR_INVALID, "prologue is NULL");

@@ -15,13 +15,15 @@
  * so transposed [B, T, H, D] storage needs no copy.
  *
  * Conventions shared by every entry point:
- *   - All pointers are device pointers, allocated by the caller.  The library allocates nothing, keeps no
- *     device memory between calls and never throws across this boundary.
+ *   - All pointers are device pointers, allocated by the caller.  The library allocates nothing and never throws
+ *     across this boundary; the only device memory it keeps between calls is the fixed scratch array of
+ *     gdr_chunk_fwd_noalloc (on each GPU where that entry point has run).
  *   - Work is enqueued asynchronously on `stream`; no entry point synchronises the device.
  *   - Inputs are never written.  `h0` may alias `ht` (in-place state update); no other aliasing is allowed.
  *   - Return value: GDR_OK (0), or a negative gdr_status.  gdr_last_error() returns a thread-local message
  *     describing the last failure of the calling thread.
- *   - Entry points are re-entrant and thread-safe.
+ *   - Entry points are re-entrant and thread-safe (gdr_chunk_fwd_noalloc: calls that overlap in time on one GPU share
+ *     its scratch and must be serialised by the caller).
  */
 #ifndef GDR_H
 #define GDR_H
@@ -133,6 +135,22 @@ int gdr_chunk_fwd_fused(const gdr_args* args, const gdr_prologue* pro, hipStream
  * (src/ops/kimi_delta_attention.py:540-553).  For B=4, T=4096, H=16, K=V=128 it is 291.5 MB (71,168 bytes per
  * chunk and head). */
 int64_t gdr_chunk_workspace_bytes(const gdr_args* args);
+
+/* Size of the device scratch behind gdr_chunk_fwd_noalloc (128 MiB per GPU). */
+#define GDR_NOALLOC_SCRATCH_BYTES (128LL << 20)
+
+/* gdr_chunk_fwd without a workspace and without any allocation: the two-launch path runs on a scratch array of
+ * GDR_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on, from the first call on that GPU until the
+ * process ends.  No counterpart in the reference (whose op allocates its intermediates per call,
+ * src/ops/kimi_delta_attention.py:540-553): it is for callers that cannot allocate device memory -- code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.  Calls no hipMalloc, hipFree or
+ * allocating library routine.  args->workspace must be NULL; a call whose gdr_chunk_workspace_bytes exceeds
+ * GDR_NOALLOC_SCRATCH_BYTES (e.g. more than 1,885 chunk-head records at K = V = 128: B = 1, T = 4096, H = 16 fits)
+ * returns GDR_ERR_UNSUPPORTED.  Nothing in the scratch needs clearing: the preparation launch writes every record
+ * the scan launch of the same call reads.  All calls on one GPU share its scratch, so calls that overlap in time on
+ * one GPU (different streams, threads or processes' shared contexts) race; serialise them.  Otherwise as
+ * gdr_chunk_fwd (same kernels, bit-identical results). */
+int gdr_chunk_fwd_noalloc(const gdr_args* args, hipStream_t stream);
 
 /* Gradients of gdr_chunk_fwd for gdr_chunk_bwd.  Every tensor has the shape of its forward counterpart;
  * d_query, d_key and d_value are bf16 or f32 (any of them may differ from the forward dtype), d_gate and
