@@ -28,6 +28,8 @@
 // 16x16 blocks of (I + diag(beta) P) are inverted in fp32; W and U come out of a blocked forward substitution on
 // v_mfma_f32_16x16x16_bf16 with fp32 accumulation.  W, U, Q e^B and K e^{B_end - B} are stored as bf16, as the
 // reference stores W, U and u.
+#include <atomic>
+
 #include "chunk_common.h"
 #include "gdr_internal.h"
 #include "split_common.h"
@@ -750,26 +752,34 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
   }
 }
 
-// =============================== scan: one workgroup per (sequence, head) x 64 columns ===============================
-constexpr int kScanTiles = 1;                          // 16-column tiles per compute wave
-constexpr int kScanCompute = kScanSlice / (16 * kScanTiles);  // compute waves per scan workgroup
-constexpr int kScanLoaders = 4;                        // loader waves per scan workgroup
-constexpr int kScanThreads = 64 * (kScanCompute + kScanLoaders);
-constexpr int kOP = kScanSlice + 8;  // row pitch (elements) of the scan's output tile in LDS
+// ============================ scan: one workgroup per (sequence, head) x SL value columns ============================
+// SL (16, 32 or 64 columns) is chosen per launch so that the workgroups cover the CUs: every compute wave owns 16
+// state columns and reads the whole record's W, Q e^B and K e^{B_end - B} from LDS each step, so narrower slices mean
+// fewer compute waves per CU sharing its LDS bandwidth and more CUs at work.
+template <int SL, int NT>
+struct ScanShape {
+  static constexpr int kCompute = SL / (16 * NT);                // compute waves, NT 16-column state tiles each
+  static constexpr int kLoaders = 4;                             // loader waves
+  static constexpr int kThreads = 64 * (kCompute + kLoaders);
+  static constexpr int kOP = SL + 8;                             // row pitch (elements) of the output tile in LDS
+};
 
 // kStates (backward recompute): instead of the output, write the fp32 state entering every chunk (and the final
 // one) to `states` [NC + 1][K][V] and the bf16 u to `ubuf` [NC * 64][V], per (sequence, head).
-template <int VARIANT, int K, typename OutT, bool kStates = false>
-__global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_args a, int n_slices, int xcd_map,
-                                                                     int nc, int64_t rec_bytes,
-                                                                     float* __restrict__ states,
-                                                                     __bf16* __restrict__ ubuf) {
+template <int VARIANT, int K, typename OutT, int SL, int NT, bool kStates = false>
+__global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_kernel(const gdr_args a, int n_slices,
+                                                                                int xcd_map, int nc,
+                                                                                int64_t rec_bytes,
+                                                                                float* __restrict__ states,
+                                                                                __bf16* __restrict__ ubuf) {
   constexpr bool kDelta = VARIANT != GDR_GLA;
-  constexpr int KT = K / 16, KS = K / 32, NT = kScanTiles;
+  constexpr int KT = K / 16, KS = K / 32;
+  constexpr int kScanCompute = ScanShape<SL, NT>::kCompute, kOP = ScanShape<SL, NT>::kOP;
+  constexpr int kScanLoaders = ScanShape<SL, NT>::kLoaders;
   using R = Rec<K>;
 
-  constexpr int SB = R::FIX + R::UT_SLICE;         // LDS bytes per buffer
-  constexpr int NF = R::FIX / 16, NU = R::UT_SLICE / 16;
+  constexpr int SB = R::FIX + R::ut_slice(SL);     // LDS bytes per buffer
+  constexpr int NF = R::FIX / 16, NU = R::ut_slice(SL) / 16;
   constexpr int NG = ((NF + NU + 63) / 64 + kScanLoaders - 1) / kScanLoaders;  // 64-piece groups per loader wave
   extern __shared__ __align__(16) unsigned char smem[];
 
@@ -793,7 +803,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
     bidx = 0;
   }
   const int nchunks = (len + kChunk - 1) / kChunk;
-  const int v0 = slice * kScanSlice;
+  const int v0 = slice * SL;
   const unsigned char* ws = static_cast<const unsigned char*>(a.workspace);
   // wave index made explicitly wave-uniform so that role and group branches are scalar branches
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -820,13 +830,35 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
         }
       }
     };
+    // The compute waves leave each chunk's output in a double-buffered LDS tile [64][kOP]; the loaders store the
+    // previous chunk's tile during the next step as whole SL-column rows with 16-byte stores.
+    const OutT* otile = reinterpret_cast<const OutT*>(smem + 2 * SB);
+    OutT* op = static_cast<OutT*>(const_cast<void*>(a.out.ptr)) + bidx * a.out.stride_b + h * a.out.stride_h +
+               bos * a.out.stride_t;
+    auto store_tile = [&](int chunk) {
+      constexpr int kPer = 16 / int(sizeof(OutT)), kRowPieces = SL / kPer;
+      const OutT* tl = otile + (chunk & 1) * 64 * kOP;
+#pragma unroll
+      for (int pc = lw * 64 + lane; pc < 64 * kRowPieces; pc += 64 * kScanLoaders) {
+        const int row = pc / kRowPieces, col = (pc % kRowPieces) * kPer;
+        const uint4 v = *reinterpret_cast<const uint4*>(tl + row * kOP + col);
+        const int tk = chunk * kChunk + row;
+        if (tk < len) *reinterpret_cast<uint4*>(op + int64_t(tk) * a.out.stride_t + v0 + col) = v;
+      }
+    };
     if (nchunks > 0) copy_record(0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     lds_barrier();
     for (int s = 0; s < nchunks; ++s) {
       if (s + 1 < nchunks) copy_record(s + 1, (s + 1) & 1);  // buffer (s + 1) & 1 held chunk s - 1: done
+      if constexpr (!kStates) {
+        if (s > 0) store_tile(s - 1);
+      }
       __builtin_amdgcn_s_waitcnt(0);
       lds_barrier();
+    }
+    if constexpr (!kStates) {
+      if (nchunks > 0) store_tile(nchunks - 1);
     }
     return;
   }
@@ -835,9 +867,6 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
   const int l16 = lane & 15, g4 = lane >> 4;
   const int c0 = v0 + 16 * NT * wave;  // first column of this wave
   const size_t sbase = size_t(n * H + h) * K * a.value_dim;
-  OutT* op = static_cast<OutT*>(const_cast<void*>(a.out.ptr)) + bidx * a.out.stride_b + h * a.out.stride_h +
-             bos * a.out.stride_t;
-  const int64_t o_st = a.out.stride_t;
   floatx4 st[NT][KT];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -861,32 +890,19 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
           states[st_base + (size_t(c) * K + 16 * m + 4 * g4 + r) * V + c0 + 16 * t + l16] = st[t][m][r];
   };
 
-  // The output of a chunk goes through LDS: the compute waves write their 16-column stripes into the chunk's tile
-  // (double-buffered, [64][kOP]), and after the step's barrier wave w stores rows 16 w .. 16 w + 15 of the previous
-  // chunk as whole 64-column rows with 16-byte stores (instead of 16 row pieces of 32 bytes per store).
   OutT* otile = reinterpret_cast<OutT*>(smem + 2 * SB);
-  auto store_tile = [&](int chunk) {
-    constexpr int kPer = 16 / int(sizeof(OutT)), kRowPieces = kScanSlice / kPer, kRows = 64 / kRowPieces;
-    const OutT* tl = otile + (chunk & 1) * 64 * kOP;
-#pragma unroll
-    for (int u = 0; u < 16 / kRows; ++u) {
-      const int row = 16 * wave + kRows * u + lane / kRowPieces, pc = lane % kRowPieces;
-      const uint4 v = *reinterpret_cast<const uint4*>(tl + row * kOP + pc * kPer);
-      const int tk = chunk * kChunk + row;
-      if (tk < len) *reinterpret_cast<uint4*>(op + tk * o_st + v0 + pc * kPer) = v;
-    }
-  };
   for (int s = 0; s < nchunks; ++s) {
     const unsigned char* bb = smem + (s & 1) * SB;
     if constexpr (kStates) store_state(s);
-    if constexpr (!kStates) {
-      if (s > 0) store_tile(s - 1);
-    }
     const __bf16* wl = reinterpret_cast<const __bf16*>(bb + R::W);
     const __bf16* ql = reinterpret_cast<const __bf16*>(bb + R::QD);
     const __bf16* scl = reinterpret_cast<const __bf16*>(bb + R::SC);
     const float* gam = reinterpret_cast<const float*>(bb + R::GAM);
     const __bf16* utl = reinterpret_cast<const __bf16*>(bb + R::FIX);  // UT rows of this slice
+
+    // Every LDS read of the step is issued ahead of its use, in the order of use (LDS reads return in order):
+    // W / Q e^B fragments one row block ahead, the U rows with the first block, the score tiles and the first two
+    // K e^{B_end - B} tiles (with their gamma) during the last block, each further Kt tile two tiles ahead.
 
     // state as the bf16 B operand: two accumulator tiles = one 32-deep k slot set {32kk + 4g4 + r, +16}
     bf16x8 sB[NT][KS];
@@ -900,8 +916,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
     // with four consecutive output columns of one token.  Every A fragment read from LDS feeds NT tiles.
     floatx4 acc_ot[NT][4];
     bf16x4 ub[NT][4];
-    // A fragments of row block i (Q e^B and W, k slots {32kk + 4g4 + r, +16}), read one block ahead
-    bf16x8 fq[2][KS], fw[2][KS];
+    bf16x8 fq[2][KS], fw[2][KS];  // A fragments of row block i (k slots {32kk + 4g4 + r, +16})
     auto read_block = [&](int i, int buf) {
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
@@ -910,11 +925,41 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
         if constexpr (kDelta) fw[buf][kk] = *reinterpret_cast<const bf16x8*>(wl + r0);
       }
     };
+    bf16x8 fk[3][2];  // Kt^T fragments of state tile m (transposing reads of the row-major tile), ring of 3
+    float4 gm[3];     // gamma of the same rows
+    auto read_kt = [&](int m) {
+      const int buf = m % 3;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int tok = 32 * kk + 4 * g4 + (l16 >> 2);
+        const int chn = 16 * m + 4 * (l16 & 3);
+        const int off = (s & 1) * SB + R::KT;
+        fk[buf][kk] = concat(lds_read_tr(smem, off + R::rk(tok, chn) * 2),
+                             lds_read_tr(smem, off + R::rk(tok + 16, chn) * 2));
+      }
+      gm[buf] = *reinterpret_cast<const float4*>(gam + 16 * m + 4 * g4);
+    };
+    bf16x4 fsc[10];
     read_block(0, 0);
+    bf16x4 uu[NT][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        uu[t][i] = *reinterpret_cast<const bf16x4*>(utl + R::rt(c0 - v0 + 16 * t + l16, 16 * i + 4 * g4));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (i + 1 < 4) read_block(i + 1, (i + 1) & 1);
-      __builtin_amdgcn_sched_barrier(0);  // keep the next block's reads ahead of this block's MFMAs
+      if (i + 1 < 4) {
+        read_block(i + 1, (i + 1) & 1);
+      } else {
+        if constexpr (!kStates) {
+#pragma unroll
+          for (int q = 0; q < 10; ++q) fsc[q] = *reinterpret_cast<const bf16x4*>(scl + q * 256 + l16 * 16 + 4 * g4);
+        }
+        read_kt(0);
+        read_kt(1);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of this block's MFMAs
       floatx4 ax[NT], ao[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) ax[t] = ao[t] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -928,10 +973,9 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const bf16x4 uu = *reinterpret_cast<const bf16x4*>(utl + R::rt(c0 - v0 + 16 * t + l16, 16 * i + 4 * g4));
         floatx4 u;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) u[r] = kDelta ? f32(uu[r]) - ax[t][r] : f32(uu[r]);
+        for (int r = 0; r < 4; ++r) u[r] = kDelta ? f32(uu[t][i][r]) - ax[t][r] : f32(uu[t][i][r]);
         ub[t][i] = pack4(u);
         acc_ot[t][i] = ao[t];
         if constexpr (kStates) {
@@ -941,43 +985,38 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
         }
       }
     }
-    // O_i^T += u_j^T Sc_ij^T: u_j's accumulator layout is the A layout of u_j^T; Sc_ij^T is read like Sc_ij as A
+    // O_i^T += u_j^T Sc_ij^T over j <= i, two 16-token blocks per 32-deep MFMA: the concatenated accumulator layouts
+    // of u_j, u_{j+1} are the A layout of [u_j u_{j+1}]^T in the two-tile k order, and the score tiles read like
+    // Sc_ij give B in the same order (a block past i contributes zeros).  Every MFMA accumulating onto the readout
+    // has the readout's shape, so no accumulator passes between MFMAs of different shapes.
     if constexpr (!kStates) {
-      bf16x4 fsc[10];
-#pragma unroll
-      for (int q = 0; q < 10; ++q) fsc[q] = *reinterpret_cast<const bf16x4*>(scl + q * 256 + l16 * 16 + 4 * g4);
+      const bf16x4 z4 = {};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j <= i; ++j)
+        for (int j = 0; j <= i; j += 2)
 #pragma unroll
-          for (int t = 0; t < NT; ++t) acc_ot[t][i] = mfma16(ub[t][j], fsc[tri_tile(i, j)], acc_ot[t][i]);
+          for (int t = 0; t < NT; ++t) {
+            const bool pair = j + 1 <= i;
+            acc_ot[t][i] = mfma32(concat(ub[t][j], pair ? ub[t][j + 1] : z4),
+                                  concat(fsc[tri_tile(i, j)], pair ? fsc[tri_tile(i, j + 1)] : z4), acc_ot[t][i]);
+          }
     }
-    // S = diag(gamma) S + Kt^T u, Kt^T read transposed from the row-major tile, one tile ahead
-    bf16x8 fk[2][2];
-    auto read_kt = [&](int m, int buf) {
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const int tok = 32 * kk + 4 * g4 + (l16 >> 2);
-        const int chn = 16 * m + 4 * (l16 & 3);
-        const int off = (s & 1) * SB + R::KT;
-        fk[buf][kk] = concat(lds_read_tr(smem, off + R::rk(tok, chn) * 2), lds_read_tr(smem, off + R::rk(tok + 16, chn) * 2));
-      }
-    };
-    read_kt(0, 0);
+    // S = diag(gamma) S + Kt^T u
 #pragma unroll
     for (int m = 0; m < KT; ++m) {
-      if (m + 1 < KT) read_kt(m + 1, (m + 1) & 1);
+      if (m + 2 < KT) read_kt(m + 2);
       __builtin_amdgcn_sched_barrier(0);
-      const float4 gm = *reinterpret_cast<const float4*>(gam + 16 * m + 4 * g4);
+      const float4 g = gm[m % 3];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        st[t][m][0] *= gm.x; st[t][m][1] *= gm.y; st[t][m][2] *= gm.z; st[t][m][3] *= gm.w;
+        st[t][m][0] *= g.x; st[t][m][1] *= g.y; st[t][m][2] *= g.z; st[t][m][3] *= g.w;
       }
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) st[t][m] = mfma32(fk[m & 1][kk], concat(ub[t][2 * kk], ub[t][2 * kk + 1]), st[t][m]);
+        for (int t = 0; t < NT; ++t)
+          st[t][m] = mfma32(fk[m % 3][kk], concat(ub[t][2 * kk], ub[t][2 * kk + 1]), st[t][m]);
     }
     // output: lane holds O[token 16 i + l16][columns c0 + 16 t + 4 g4 .. + 3], into the chunk's LDS tile
     if constexpr (!kStates) {
@@ -988,9 +1027,6 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(const gdr_a
         for (int t = 0; t < NT; ++t) store4(tw + (16 * i + l16) * kOP + (c0 - v0) + 16 * t + 4 * g4, acc_ot[t][i]);
     }
     lds_barrier();
-  }
-  if constexpr (!kStates) {
-    if (nchunks > 0) store_tile(nchunks - 1);
   }
   if constexpr (kStates) store_state(nchunks);
   if (a.ht) {
@@ -1022,12 +1058,59 @@ hipError_t launch_prep(const gdr_args& a, const gdr_prologue& pro, hipStream_t s
   return hipGetLastError();
 }
 
+// Compute units of the current device (queried once per device; 256 on MI355X).
+int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cus[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Value columns per scan workgroup: the widest slice (fewest record copies into LDS) whose workgroups still cover
+// every CU, else the narrowest.
+int scan_slice(int64_t bh, int value_dim) {
+  const int64_t cus = device_cus();
+  for (int sl : {64, 32})
+    if (value_dim % sl == 0 && bh * (value_dim / sl) >= cus) return sl;
+  return 16;
+}
+
+template <int VARIANT, int K, typename OutT, int SL, int NT, bool kStates>
+hipError_t launch_scan_sl(const gdr_args& a, int nc, float* states, __bf16* ubuf, hipStream_t stream) {
+  using Sh = ScanShape<SL, NT>;
+  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::ut_slice(SL)) + (kStates ? 0 : 2 * 64 * Sh::kOP * int(sizeof(OutT)));
+  static_assert(scan_lds <= 160 * 1024, "scan LDS");
+  constexpr auto kernel = &chunk_scan_kernel<VARIANT, K, OutT, SL, NT, kStates>;
+  hipError_t e = configure_lds<kernel>(scan_lds);
+  if (e != hipSuccess) return e;
+  const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
+  const int bh = n_seq * a.heads;
+  const int n_slices = a.value_dim / SL;
+  const int xcd_map = (bh % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL(kernel, dim3(bh * n_slices), dim3(Sh::kThreads), scan_lds, stream, a, n_slices, xcd_map, nc,
+                     Rec<K>::bytes(a.value_dim), states, ubuf);
+  return hipGetLastError();
+}
+
+template <int VARIANT, int K, typename OutT, bool kStates>
+hipError_t launch_scan(const gdr_args& a, float* states, __bf16* ubuf, hipStream_t stream) {
+  const int nc = (a.seq_len + kChunk - 1) / kChunk;
+  const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
+  switch (scan_slice(int64_t(n_seq) * a.heads, a.value_dim)) {
+    case 64: return launch_scan_sl<VARIANT, K, OutT, 64, 1, kStates>(a, nc, states, ubuf, stream);
+    case 32: return launch_scan_sl<VARIANT, K, OutT, 32, 1, kStates>(a, nc, states, ubuf, stream);
+    default: return launch_scan_sl<VARIANT, K, OutT, 16, 1, kStates>(a, nc, states, ubuf, stream);
+  }
+}
+
 template <int VARIANT, int K, typename OutT>
 hipError_t launch_split_typed(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
-  const int nc = (a.seq_len + kChunk - 1) / kChunk;
-  const int64_t rec = Rec<K>::bytes(a.value_dim);
-  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::UT_SLICE) + 2 * 64 * kOP * int(sizeof(OutT));
-  static_assert(scan_lds <= 160 * 1024, "scan LDS");
   hipError_t e;
   const bool conv = pro.flags & GDR_PRO_CONV;
   if (!pro.flags) {
@@ -1040,15 +1123,8 @@ hipError_t launch_split_typed(const gdr_args& a, const gdr_prologue& pro, hipStr
   } else {
     e = conv ? launch_prep<VARIANT, K, 5>(a, pro, stream) : launch_prep<VARIANT, K, 1>(a, pro, stream);
   }
-  if (e == hipSuccess) e = configure_lds<&chunk_scan_kernel<VARIANT, K, OutT>>(scan_lds);
   if (e != hipSuccess) return e;
-  const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
-  const int bh = n_seq * a.heads;
-  const int n_slices = a.value_dim / kScanSlice;
-  const int xcd_map = (bh % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((chunk_scan_kernel<VARIANT, K, OutT>), dim3(bh * n_slices), dim3(kScanThreads), scan_lds,
-                     stream, a, n_slices, xcd_map, nc, rec, nullptr, nullptr);
-  return hipGetLastError();
+  return launch_scan<VARIANT, K, OutT, false>(a, nullptr, nullptr, stream);
 }
 
 template <int VARIANT, int K>
@@ -1071,19 +1147,10 @@ hipError_t launch_states_typed(const gdr_args& fwd, const BwdLayout& L, unsigned
   gdr_args a = fwd;
   a.workspace = ws + L.rec;
   a.ht = nullptr;
-  const int nc = (a.seq_len + kChunk - 1) / kChunk;
-  const int64_t rec = Rec<K>::bytes(a.value_dim);
-  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::UT_SLICE);
   hipError_t e = launch_prep<VARIANT, K, 0>(a, gdr_prologue{}, stream);
-  if (e == hipSuccess) e = configure_lds<&chunk_scan_kernel<VARIANT, K, __bf16, true>>(scan_lds);
   if (e != hipSuccess) return e;
-  const int bh = a.batch * a.heads;
-  const int n_slices = a.value_dim / kScanSlice;
-  const int xcd_map = (bh % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((chunk_scan_kernel<VARIANT, K, __bf16, true>), dim3(bh * n_slices), dim3(kScanThreads),
-                     scan_lds, stream, a, n_slices, xcd_map, nc, rec, reinterpret_cast<float*>(ws + L.states),
-                     reinterpret_cast<__bf16*>(ws + L.ubuf));
-  return hipGetLastError();
+  return launch_scan<VARIANT, K, __bf16, true>(a, reinterpret_cast<float*>(ws + L.states),
+                                              reinterpret_cast<__bf16*>(ws + L.ubuf), stream);
 }
 
 template <int VARIANT>

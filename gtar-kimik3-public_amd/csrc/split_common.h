@@ -7,7 +7,7 @@
 namespace gdr {
 namespace chunk {
 
-constexpr int kScanSlice = 64;  // value columns per scan workgroup
+constexpr int kScanSlice = 64;  // value columns per reverse-scan (backward) workgroup
 
 // Workspace record of one (chunk, head); byte offsets.  UT (U^T, [V][64]) closes the record.  Rows are unpadded;
 // 16-byte chunks are XOR-swizzled within a row instead (chunk c of row r stored at chunk c ^ (r mod chunks per
@@ -24,7 +24,7 @@ struct Rec {
   static constexpr int SC = KT + 64 * K * 2;                    // bf16 [10][16][16] scale x gated scores, tile (i, j <= i)
   static constexpr int GAM = SC + 10 * 256 * 2;                 // fp32 [K] e^{B_end}
   static constexpr int FIX = ((GAM + K * 4 + 255) / 256) * 256;  // start of UT
-  static constexpr int UT_SLICE = kScanSlice * 64 * 2;          // bytes of 64 rows of UT
+  static constexpr int ut_slice(int cols) { return cols * 64 * 2; }  // bytes of `cols` rows of UT
   static int64_t bytes(int value_dim) { return FIX + ((int64_t(value_dim) * 64 * 2 + 255) / 256) * 256; }
   // element offsets of (row, column) in the swizzled [*][K] arrays and of (row, token) in UT
   static __device__ __forceinline__ int rk(int row, int col) {
