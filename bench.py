@@ -23,8 +23,13 @@ One JSON line on stdout:
     and the KDA op's share of the time.
   * train: the prefill configuration under torch.autograd, forward then backward (gdr_chunk_bwd), with the
     backward's algorithmic bytes and HBM fraction.
+  * variants: the variant sweep configuration (Gated DeltaNet, GLA, DeltaNet and KDA at B=2, T=8192, H=16,
+    dk=dv=128, bf16 q/k/v, fp32 gate/beta/state, no initial state): per op tokens/s, the HBM roofline with traffic
+    and the bf16 MFMA fraction.
   * cpu_baseline: the reference's CPU path for the op (fp32 token loop, restated in oracle/) timed on this
-    host on a bounded sample of the same prefill workload.
+    host on a bounded sample of the same prefill workload; cpu_baselines_other_configs: the same loop on c1 (in
+    full), the decode step (a bounded number of steps, per step) and each variant of the sweep (one pass over a
+    quarter of the sequence).
 Only one GPU is used; --gpus above 1 exits with a message.
 """
 
@@ -109,6 +114,66 @@ def bench_prefill(gdr, workloads, torch, steps, warmup):
         stop.record(stream)
         torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps  # ms per step (one call: prep + scan launches)
+
+
+VARIANT_SWEEP = dict(B=2, T=8192, H=16, K=128, V=128, chunk=64)
+VARIANT_FNS = {"kda": "chunk_kimi_delta_attention", "gdn": "chunk_gated_deltanet",
+               "gla": "chunk_gated_linear_attention", "deltanet": "chunk_deltanet"}
+
+
+def variant_bytes(variant, B, T, H, K, V, h0=False, **_):
+    """Algorithmic bytes of one chunk call: q, k, v (bf16) read and out (bf16) written per token and head, the gate
+    (fp32 per channel for KDA and GLA, per head for GDN, none for DeltaNet) and beta (none for GLA) read, the final
+    state written and, when given, the initial state read."""
+    bf16, f32 = 2, 4
+    gate = {"kda": K * f32, "gla": K * f32, "gdn": f32, "deltanet": 0}[variant]
+    beta = 0 if variant == "gla" else f32
+    per_token_head = 2 * K * bf16 + V * bf16 + gate + beta + V * bf16
+    return B * T * H * per_token_head + (2 if h0 else 1) * B * H * K * V * f32
+
+
+def variant_flops(variant, C, K, V):
+    """Causal FLOP count per token and head: the delta rule (delta_flops_per_token_head) or, for GLA (no delta
+    rule), the intra-chunk scores and output C*(K+V) plus the state products Q S and K^T V 4*K*V."""
+    return C * (K + V) + 4 * K * V if variant == "gla" else delta_flops_per_token_head(C, K, V)
+
+
+def bench_variants(gdr, workloads, torch, steps, warmup):
+    """The variant sweep configuration: each op at B=2, T=8192, H=16, dk=dv=128, chunk 64 (bf16 q/k/v, fp32 gate,
+    beta and state, no initial state), one call = the public chunk op with output_final_state=True."""
+    cfg = VARIANT_SWEEP
+    dev = torch.device("cuda")
+    stream = torch.cuda.current_stream()
+    out = {}
+    for variant in ("gdn", "gla", "deltanet", "kda"):
+        inp = workloads.make_inputs(variant, cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"], seed=0, device=dev)
+        fn = getattr(gdr, VARIANT_FNS[variant])
+        args = inp.args()
+        with torch.no_grad():
+            for _ in range(warmup):
+                fn(*args, output_final_state=True)
+            torch.cuda.synchronize()
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(steps):
+                fn(*args, output_final_state=True)
+            stop.record(stream)
+            torch.cuda.synchronize()
+        ms = start.elapsed_time(stop) / steps
+        tokens = cfg["B"] * cfg["T"]
+        nbytes = variant_bytes(variant, **cfg)
+        flops = variant_flops(variant, cfg["chunk"], cfg["K"], cfg["V"]) * tokens * cfg["H"]
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        tflops = flops / (ms * 1e-3) / 1e12
+        out[variant] = {"op": VARIANT_FNS[variant], "ms_per_call": round(ms, 4),
+                        "tokens_per_s": round(tokens / (ms * 1e-3), 1), "algorithmic_bytes": nbytes,
+                        "algorithmic_flops": flops, "tflops": round(tflops, 2),
+                        "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                     "traffic": committed_traffic(f"chunk_{variant}_prefill_c4")}}
+    return {"workload": "chunk_prefill_variant_sweep", **cfg, "state": "fp32", "initial_state": None,
+            "variants": out}
 
 
 def bench_decode(gdr, workloads, torch, warmup):
@@ -435,25 +500,68 @@ def bench_train(gdr, workloads, torch, steps, warmup):
             "backward_traffic": committed_traffic("chunk_kda_backward")}
 
 
+def _timed_passes(fn, budget_s):
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        passes += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= budget_s:
+            return passes, elapsed
+
+
 def cpu_baseline(workloads, torch, budget_s):
-    """The reference CPU path (fp32 token loop) on the full prefill workload, repeated until `budget_s`."""
+    """The reference CPU path for the op (the fp32 token loop, restated in oracle/) on the full prefill workload,
+    repeated until `budget_s`."""
     from oracle import gdr_oracle as oracle
 
     cfg = PREFILL
     inp = workloads.make_inputs("kda", cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"], seed=0, state_std=0.02)
-    passes, t0 = 0, time.perf_counter()
-    while True:
-        oracle.kda_reference(inp.query, inp.key, inp.value, inp.gate, inp.beta, None, inp.initial_state)
-        passes += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed >= budget_s:
-            break
+    passes, elapsed = _timed_passes(lambda: oracle.kda_reference(inp.query, inp.key, inp.value, inp.gate, inp.beta,
+                                                                 None, inp.initial_state), budget_s)
     tokens = passes * cfg["B"] * cfg["T"]
     return {"value": round(tokens / elapsed, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"{passes} full pass(es) of the prefill workload (B=4 T=4096 H=16 dk=dv=128) through the "
                       f"reference's fp32 CPU token loop, {elapsed:.1f} s, {len(os.sched_getaffinity(0))} host "
                       "cores visible"}
+
+
+def cpu_baselines_other(workloads, torch, budget_s):
+    """The same CPU token loop on the other configurations: c1 (the reference's CPU-runnable case, fp32 B=1 T=256
+    H=2 d=64) in full, repeated until `budget_s`; the batch-256 decode step over a bounded number of steps (about
+    `budget_s`), reported per step; and each variant of the sweep configuration (B=2 H=16 d=128) with its own update
+    rule (the reference's unified loop, tests/bench_ops.py:52-66), one pass over the first quarter of the sequence."""
+    from oracle import gdr_oracle as oracle
+
+    res = {"cores": torch.get_num_threads(), "host_cores_visible": len(os.sched_getaffinity(0)), "kind": "port"}
+    c1 = workloads.make_inputs("kda", 1, 256, 2, 64, 64, seed=0, dtype=torch.float32)
+    passes, elapsed = _timed_passes(lambda: oracle.kda_reference(c1.query, c1.key, c1.value, c1.gate, c1.beta),
+                                    budget_s)
+    res["c1_kda_fp32_B1_T256_H2_d64"] = {"tokens_per_s": round(passes * 256 / elapsed, 1),
+                                         "ms_per_pass": round(elapsed / passes * 1e3, 2), "passes": passes}
+    cfg = DECODE
+    dec = workloads.decode_inputs("kda", cfg["B"], cfg["H"], cfg["K"], cfg["V"], seed=100)
+    state = [workloads.decode_state(cfg["B"], cfg["H"], cfg["K"], cfg["V"], std=0.02, seed=7)]
+
+    def step():
+        _, state[0] = oracle.kda_reference(dec.query, dec.key, dec.value, dec.gate, dec.beta, None, state[0])
+
+    steps, elapsed = _timed_passes(step, budget_s)
+    res["c3_kda_decode_B256_H16_d128"] = {"ms_per_step": round(elapsed / steps * 1e3, 2), "steps": steps,
+                                          "tokens_per_s": round(cfg["B"] * steps / elapsed, 1),
+                                          "state_gb_per_s": round(decode_bytes(**cfg) * steps / elapsed / 1e9, 2)}
+    vs, t_sample = VARIANT_SWEEP, VARIANT_SWEEP["T"] // 4
+    for variant in ("gdn", "gla", "deltanet"):
+        inp = workloads.make_inputs(variant, vs["B"], t_sample, vs["H"], vs["K"], vs["V"], seed=0)
+        t0 = time.perf_counter()
+        oracle.recurrence(variant, inp.query, inp.key, inp.value, inp.gate, inp.beta, dtype=torch.float32)
+        elapsed = time.perf_counter() - t0
+        res[f"c4_{variant}_B2_H16_d128"] = {"tokens_per_s": round(vs["B"] * t_sample / elapsed, 1),
+                                            "sample": f"one pass over the first {t_sample} of the {vs['T']} tokens "
+                                                      f"(the loop's cost per token does not depend on T), "
+                                                      f"{elapsed:.1f} s"}
+    return res
 
 
 def main():
@@ -468,6 +576,7 @@ def main():
     ap.add_argument("--no-stack", action="store_true", help="skip the hybrid stack harness leg")
     ap.add_argument("--no-varlen", action="store_true", help="skip the packed varlen prefill leg")
     ap.add_argument("--no-train", action="store_true", help="skip the forward + backward (autograd) leg")
+    ap.add_argument("--no-variants", action="store_true", help="skip the GDN / GLA / DeltaNet variant sweep leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="minimum seconds of CPU baseline work")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the GPU legs, copy a buffer of this many MiB three times (a plain copy kernel of "
@@ -514,6 +623,8 @@ def main():
         "algorithmic_bytes": nbytes,
         "algorithmic_flops": flops,
     }
+    if not opts.no_variants:
+        record["variants"] = bench_variants(gdr, workloads, torch, steps=20, warmup=5)
     if not opts.no_decode:
         record["decode"] = bench_decode(gdr, workloads, torch, warmup=20)
     if not opts.no_verify:
@@ -534,6 +645,7 @@ def main():
         torch.cuda.synchronize()
     if not opts.no_cpu:
         record["cpu_baseline"] = cpu_baseline(workloads, torch, opts.cpu_budget)
+        record["cpu_baselines_other_configs"] = cpu_baselines_other(workloads, torch, opts.cpu_budget / 4)
     print(json.dumps(record), flush=True)
 
 

@@ -3,7 +3,10 @@
 Mirrors the reference's per-op host code (src/ops/kimi_delta_attention.py:625-692 and the identical helpers in
 gated_deltanet.py:472-520, gated_linear_attention.py:437-483, deltanet.py:399-445):
   * scale = `scale or head_dim ** -0.5` (so 0.0 also selects the default, as in the reference),
-  * the chunk path casts q, k, v to the autocast dtype when autocast is enabled (utils.py:84-88),
+  * the chunk path casts q, k, v to the autocast dtype when autocast is enabled (utils.py:84-88), and takes its
+    matrix-product operands in k's dtype as the reference's kernels do (.to(k.dtype)): bf16 and f16 q, k, v run the
+    chunk kernels on bf16 / f16 MFMA operands, and fp32 q, k, v run the recurrent kernel over the whole sequence,
+    all in fp32 (the chunk backward takes bf16 only),
   * a missing initial state is a zero fp32 state, a given one is used as `initial_state.float().contiguous()`,
   * the final state is always a fresh fp32 tensor and inputs are never modified,
   * the output has the value's dtype; `(out, final_state)` is returned only when `output_final_state`.
@@ -102,12 +105,26 @@ def run(variant: int, chunk: bool, query, key, value, gate, beta, scale, initial
             raise ValueError(f"{name}: initial_state must have shape {state_shape}, got {tuple(initial_state.shape)}")
         initial_state = initial_state.float().contiguous()
 
+    exact_f32 = chunk and any(x.dtype not in _OPERAND_DTYPES for x in (query, key, value))
+    if exact_f32:
+        # The reference's chunk kernels take their dot operands in the input dtype (.to(k.dtype),
+        # kimi_delta_attention.py:99-100, :130, :135): fp32 inputs get fp32 products.  The chunk kernels multiply
+        # 16-bit operands, so fp32 input runs the recurrence instead (every product and sum in fp32).
+        if grad:
+            raise NotImplementedError(f"{name}: fp32 q, k, v run the exact fp32 recurrence, which has no backward; "
+                                      "for training pass bfloat16 q, k, v (or run under torch.autocast(bfloat16))")
+        return _exact_f32(variant, query, key, value, gate, beta, scale, initial_state, output_final_state,
+                          cu_seqlens, out_dtype, state_shape)
     if not chunk and not (query.dtype == key.dtype == value.dtype == torch.bfloat16):
         # The recurrent kernel reads q, k, v as one element type: all bf16, or else all fp32 (an exact widening).
         query, key, value = (x if x.dtype == torch.float32 else x.float() for x in (query, key, value))
     if chunk:
-        # The chunk kernel runs its matrix products in bf16 on MFMA; it reads bf16 q, k, v with 16-byte rows.
-        query, key, value = (x.to(torch.bfloat16) for x in (query, key, value))
+        # The chunk kernels take their MFMA operands in k's dtype, bf16 or f16, as the reference casts its dot
+        # operands to k.dtype; they read q, k, v with 16-byte rows.
+        query, value = query.to(key.dtype), value.to(key.dtype)
+        if grad and key.dtype != torch.bfloat16:
+            raise NotImplementedError(f"{name}: the chunk backward runs on bfloat16 q, k, v (got {key.dtype}); for "
+                                      "training pass bfloat16 inputs or run under torch.autocast(bfloat16)")
         query, key, value = (_as_row_aligned(x) for x in (query, key, value))
         if gate is not None and variant != _lib.GDN:
             gate = _as_row_aligned(gate)
@@ -122,6 +139,37 @@ def run(variant: int, chunk: bool, query, key, value, gate, beta, scale, initial
     args = _lib.make_args(variant, query, key, value, gate, beta, out, scale, initial_state, final_state, cu_seqlens)
     workspace = _lib.chunk_workspace(args, device) if chunk else None  # noqa: F841 (alive until enqueued)
     _lib.launch("gdr_chunk_fwd" if chunk else "gdr_recurrent_fwd", args, device)
+    return (out, final_state) if output_final_state else out
+
+
+_OPERAND_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def _exact_f32(variant, query, key, value, gate, beta, scale, initial_state, output_final_state, cu_seqlens,
+               out_dtype, state_shape):
+    """The chunk op on fp32 q, k, v: libgdr's recurrent kernel over all T tokens, which keeps the state, every
+    product and every sum in fp32 (the chunkwise form is an exact regrouping of this recurrence).  Packed sequences
+    run one recurrent call each."""
+    device = query.device
+    query, key, value = (x.float() for x in (query, key, value))
+    out = torch.empty(*query.shape[:3], value.shape[-1], device=device, dtype=out_dtype)
+    final_state = torch.empty(state_shape, device=device, dtype=torch.float32) if output_final_state else None
+    if cu_seqlens is None:
+        spans = [(slice(None), None)]
+    else:
+        bounds = cu_seqlens.tolist()
+        spans = [(slice(bounds[i], bounds[i + 1]), i) for i in range(len(bounds) - 1)]
+    for span, n in spans:
+        pick = (lambda x: x) if n is None else (lambda x: x[n:n + 1])
+        cut = lambda x: None if x is None else x[:, :, span]
+        h0 = None if initial_state is None else pick(initial_state)
+        ht = None if final_state is None else pick(final_state)
+        if n is not None and bounds[n + 1] == bounds[n]:  # an empty sequence keeps its state
+            if ht is not None:
+                ht.copy_(h0 if h0 is not None else torch.zeros_like(ht))
+            continue
+        args = _lib.make_args(variant, cut(query), cut(key), cut(value), cut(gate), cut(beta), cut(out), scale, h0, ht)
+        _lib.launch("gdr_recurrent_fwd", args, device)
     return (out, final_state) if output_final_state else out
 
 

@@ -10,24 +10,55 @@ namespace chunk {
 constexpr int kChunk = 64;      // tokens per chunk
 constexpr float kHotSpan = 60.f;  // a channel whose 16-row decay span exceeds this is handled elementwise
 
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4;
+
+// MFMA operand vectors of the two 16-bit operand types (bf16 for bf16 inputs, f16 for f16 inputs).
+template <typename T> struct OpVec;
+template <> struct OpVec<__bf16> { using v8 = bf16x8; using v4 = bf16x4; };
+template <> struct OpVec<_Float16> { using v8 = f16x8; using v4 = f16x4; };
+template <typename T> using vec8 = typename OpVec<T>::v8;
+template <typename T> using vec4 = typename OpVec<T>::v4;
+
 __device__ __forceinline__ floatx4 mfma32(bf16x8 a, bf16x8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ floatx4 mfma16(bf16x4 a, bf16x4 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ floatx4 mfma32(f16x8 a, f16x8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx4 mfma16(f16x4 a, f16x4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ __bf16 bf(float x) { return static_cast<__bf16>(x); }
+template <typename T>
+__device__ __forceinline__ T cv(float x) { return static_cast<T>(x); }  // round to the operand type
 __device__ __forceinline__ float f32(__bf16 x) { return static_cast<float>(x); }
-__device__ __forceinline__ bf16x4 pack4(floatx4 v) { return bf16x4{bf(v[0]), bf(v[1]), bf(v[2]), bf(v[3])}; }
+__device__ __forceinline__ float f32(_Float16 x) { return static_cast<float>(x); }
+template <typename T = __bf16>
+__device__ __forceinline__ vec4<T> pack4(floatx4 v) { return vec4<T>{cv<T>(v[0]), cv<T>(v[1]), cv<T>(v[2]), cv<T>(v[3])}; }
 __device__ __forceinline__ bf16x8 concat(bf16x4 lo, bf16x4 hi) {
   return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
+__device__ __forceinline__ f16x8 concat(f16x4 lo, f16x4 hi) {
+  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+// Eight 16-bit values (16 bytes) of type T to fp32 (exact).
+template <typename T = __bf16>
 __device__ __forceinline__ void unpack8(uint4 raw, float* out) {
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  if constexpr (__is_same(T, __bf16)) {
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    out[2 * i] = __uint_as_float(w[i] << 16);
-    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = __uint_as_float(w[i] << 16);
+      out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else {
+    const f16x8 h = __builtin_bit_cast(f16x8, raw);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = static_cast<float>(h[i]);
   }
 }
 
@@ -36,12 +67,13 @@ __device__ __forceinline__ int strict_tile(int i, int j) { return i * (i - 1) / 
 
 // Transposing LDS read of four bf16 (ds_read_b64_tr_b16): within each 16-lane group, lane c slot r receives
 // element c % 4 of the 8 bytes addressed by lane 4 r + c / 4 of the group.
-__device__ __forceinline__ bf16x4 lds_read_tr(const unsigned char* smem, int byte_off) {
+template <typename T = __bf16>
+__device__ __forceinline__ vec4<T> lds_read_tr(const unsigned char* smem, int byte_off) {
   typedef short short4_t __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) short4_t lds_short4;
   const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (lds_short4*)((__attribute__((address_space(3))) const unsigned char*)smem + byte_off));
-  return __builtin_bit_cast(bf16x4, v);
+  return __builtin_bit_cast(vec4<T>, v);
 }
 
 // 16 bytes from global memory straight into LDS (global_load_lds_dwordx4): lane i's bytes land at the wave-uniform
@@ -61,11 +93,13 @@ __device__ __forceinline__ void lds_barrier() {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
-// Per-workgroup view of the problem: base pointers already offset to (sequence, head), strides, lengths.
-struct ChunkCtx {
-  const __bf16* qp;
-  const __bf16* kp;
-  const __bf16* vp;
+// Per-workgroup view of the problem: base pointers already offset to (sequence, head), strides, lengths.  T is the
+// element type of q, k, v.
+template <typename T>
+struct ChunkCtxT {
+  const T* qp;
+  const T* kp;
+  const T* vp;
   const float* gp;
   const float* betap;
   void* op;
@@ -76,6 +110,7 @@ struct ChunkCtx {
   float* ht;
   float scale;
 };
+using ChunkCtx = ChunkCtxT<__bf16>;
 
 // Inclusive prefix sum over the 16 lanes of each DPP row (v_add_f32 with row_shr:1, 2, 4, 8; lanes shifted in from
 // outside the row contribute 0).
@@ -87,10 +122,11 @@ __device__ __forceinline__ float row_scan16(float x) {
   return x;
 }
 
-// One channel of one row of the op's inputs, for the hot-channel fix-up: q, k (bf16) and the gate (per channel for
+// One channel of one row of the op's inputs, for the hot-channel fix-up: q, k (element type T) and the gate (per channel for
 // KDA / GLA, per token for GDN).
-struct InputRows {
-  const ChunkCtx& x;
+template <typename T>
+struct InputRowsT {
+  const ChunkCtxT<T>& x;
   int gate_mode;  // 2: per-channel gate, 1: scalar gate
   __device__ __forceinline__ void operator()(int tc, int ch, float& q, float& k, float& g) const {
     q = static_cast<float>(x.qp[tc * x.q_st + ch]);
@@ -98,6 +134,7 @@ struct InputRows {
     g = gate_mode == 2 ? x.gp[tc * x.g_st + ch] : x.gp[tc * x.g_st];
   }
 };
+using InputRows = InputRowsT<__bf16>;
 
 // Exact evaluation of the diagonal 16x16 block of the gated scores and kernel matrix for the channels whose
 // in-block decay span is too large for the block-start factorisation (hot channels; the MFMA pass gave them zero key
@@ -108,8 +145,8 @@ struct InputRows {
 // hot_mask: on lanes with lane % (K / 8) == grp, bit m marks channel 8 grp + m.  `fetch(tc, ch, q, k, g)` is called
 // by all 64 lanes (wave-uniform channel ch, tc the clamped token of row lane % 16) and returns that row's q, k and
 // gate (natural-log units) for channel ch.
-template <int K, bool kDelta, typename Fetch>
-__device__ __forceinline__ void hot_diag_fixup(int chunk_row0, int pw, int len, uint32_t hot_mask, __bf16* sc_tile,
+template <int K, bool kDelta, typename T, typename Fetch>
+__device__ __forceinline__ void hot_diag_fixup(int chunk_row0, int pw, int len, uint32_t hot_mask, T* sc_tile,
                                                float* lii_tile, const float* beta_rows, const Fetch& fetch) {
   constexpr int LPR = K / 8;
   const int lane = threadIdx.x & 63;
@@ -142,8 +179,8 @@ __device__ __forceinline__ void hot_diag_fixup(int chunk_row0, int pw, int len, 
   for (int i = 0; i < 4; ++i) {
     const int sr = s0 + i;
     if (tt >= sr) {
-      __bf16* dst = sc_tile + tt * 16 + sr;
-      *dst = bf(f32(*dst) + sc_acc[i]);
+      T* dst = sc_tile + tt * 16 + sr;
+      *dst = cv<T>(f32(*dst) + sc_acc[i]);
     }
     if (kDelta && tt > sr) lii_tile[tt * 16 + sr] += beta_rows[tt] * p_acc[i];
   }

@@ -205,12 +205,15 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
 // kPro: the fused layer prologue.  0: none (the plain op); 1: `pro.flags` selects the in-kernel q / k
 // normalisation and the beta sigmoid; 2: as 1, and the per-channel gate comes from the low-rank projection; plus 4:
 // the short convolutions of q, k, v run in the kernel too.
-template <int VARIANT, int K, int kPro = 0>
+template <int VARIANT, int K, int kPro = 0, typename T = __bf16>
 __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr_args a, int nc, int64_t rec_bytes,
                                                                        const gdr_prologue pro) {
   constexpr bool kLowRank = (kPro & 3) == 2;
   constexpr bool kConv = (kPro & 4) != 0;
   static_assert(!kLowRank || VARIANT == GDR_KDA || VARIANT == GDR_GLA, "low-rank gate: per-channel variants");
+  static_assert(kPro == 0 || __is_same(T, __bf16), "the fused prologue reads bf16 inputs");
+  using V8 = vec8<T>;
+  using V4 = vec4<T>;
   constexpr bool kDelta = VARIANT != GDR_GLA;
   constexpr int kGate = (VARIANT == GDR_KDA || VARIANT == GDR_GLA) ? 2 : (VARIANT == GDR_GDN ? 1 : 0);
   constexpr int KS = K / 32;
@@ -243,12 +246,12 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
     slot = n * nc + c;
   }
   const int bidx = a.cu_seqlens ? 0 : n;
-  ChunkCtx x;
+  ChunkCtxT<T> x;
   x.q_st = a.q.stride_t; x.k_st = a.k.stride_t; x.v_st = a.v.stride_t; x.o_st = 0;
   x.g_st = a.gate.stride_t; x.b_st = a.beta.stride_t;
-  x.qp = static_cast<const __bf16*>(a.q.ptr) + bidx * a.q.stride_b + h * a.q.stride_h + bos * x.q_st;
-  x.kp = static_cast<const __bf16*>(a.k.ptr) + bidx * a.k.stride_b + h * a.k.stride_h + bos * x.k_st;
-  x.vp = static_cast<const __bf16*>(a.v.ptr) + bidx * a.v.stride_b + h * a.v.stride_h + bos * x.v_st;
+  x.qp = static_cast<const T*>(a.q.ptr) + bidx * a.q.stride_b + h * a.q.stride_h + bos * x.q_st;
+  x.kp = static_cast<const T*>(a.k.ptr) + bidx * a.k.stride_b + h * a.k.stride_h + bos * x.k_st;
+  x.vp = static_cast<const T*>(a.v.ptr) + bidx * a.v.stride_b + h * a.v.stride_h + bos * x.v_st;
   x.gp = kGate ? static_cast<const float*>(a.gate.ptr) + bidx * a.gate.stride_b + h * a.gate.stride_h + bos * x.g_st
                : nullptr;
   x.betap = kDelta ? static_cast<const float*>(a.beta.ptr) + bidx * a.beta.stride_b + h * a.beta.stride_h +
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
   unsigned char* rec = static_cast<unsigned char*>(a.workspace) + (int64_t(slot) * H + h) * rec_bytes;
   // fused prologue: in-kernel short convolutions of q, k, v (channels h K + ch of [H K] for q, k; h V + col for v)
   constexpr bool conv = kConv;
-  const int64_t ck = int64_t(H) * K, cv = int64_t(H) * a.value_dim;
+  const int64_t ck = int64_t(H) * K, cvv = int64_t(H) * a.value_dim;
   const __bf16* cwq = static_cast<const __bf16*>(pro.conv_weight[0]) + (int64_t(h) * K) * 4;
   const __bf16* cwk = static_cast<const __bf16*>(pro.conv_weight[1]) + (int64_t(h) * K) * 4;
   const __bf16* cwv = static_cast<const __bf16*>(pro.conv_weight[2]) + (int64_t(h) * a.value_dim) * 4;
@@ -269,14 +272,14 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
     return st ? st + (int64_t(n) * nch + ch0) * 3 : nullptr;
   };
 
-  __bf16* kap = reinterpret_cast<__bf16*>(smem + L::KAP);
-  __bf16* vst = reinterpret_cast<__bf16*>(smem + L::VST);
-  __bf16* ainv = reinterpret_cast<__bf16*>(smem + L::AINV);
-  __bf16* kd = reinterpret_cast<__bf16*>(smem + L::KD);
-  __bf16* sct = reinterpret_cast<__bf16*>(smem + L::SC);
+  T* kap = reinterpret_cast<T*>(smem + L::KAP);
+  T* vst = reinterpret_cast<T*>(smem + L::VST);
+  T* ainv = reinterpret_cast<T*>(smem + L::AINV);
+  T* kd = reinterpret_cast<T*>(smem + L::KD);
+  T* sct = reinterpret_cast<T*>(smem + L::SC);
   float* epre_v = reinterpret_cast<float*>(smem + L::EPRE);
   float* etail_v = reinterpret_cast<float*>(smem + L::ETAIL);
-  __bf16* negl = reinterpret_cast<__bf16*>(smem + L::NEGL);
+  T* negl = reinterpret_cast<T*>(smem + L::NEGL);
   float* lii = reinterpret_cast<float*>(smem + L::LII);
   float* tot = reinterpret_cast<float*>(smem + L::TOT);
   float* rds = reinterpret_cast<float*>(smem + L::RDS);
@@ -307,7 +310,7 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
       const int u = min(int(threadIdx.x), 16 * w8 - 1);
       const int col = pass * K + (u % w8) * 8;
       conv4_silu8x4(x.vp + col, x.v_st, c * kChunk + 4 * (u / w8), len - 1, cwv + col * 4,
-                    state_rows(2, cv, int64_t(h) * a.value_dim + col), vpre);
+                    state_rows(2, cvv, int64_t(h) * a.value_dim + col), vpre);
     } else {
 #pragma unroll
       for (int i = 0; i < kVLoads; ++i) {
@@ -369,7 +372,7 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
         uint4 o[4];
         conv4_silu8x4((tsr ? x.kp : x.qp) + ch, tsr ? x.k_st : x.q_st, c * kChunk + 4 * rq, len - 1,
                       (tsr ? cwk : cwq) + ch * 4, state_rows(tsr, ck, int64_t(h) * K + ch), o);
-        __bf16* tile = tsr ? kd : kap;
+        T* tile = tsr ? kd : kap;
 #pragma unroll
         for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(tile + (4 * rq + i) * KP + ch) = o[i];
       }
@@ -422,8 +425,8 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       float qf[8], kf[8];
-      unpack8(qraw[kk], qf);
-      unpack8(kraw[kk], kf);
+      unpack8<T>(qraw[kk], qf);
+      unpack8<T>(kraw[kk], kf);
 #pragma unroll
       for (int j = 0; j < 8; ++j) sq += qf[j] * qf[j], sk += kf[j] * kf[j];
     }
@@ -436,11 +439,11 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       float qf[8], kf[8];
-      unpack8(qraw[kk], qf);
-      unpack8(kraw[kk], kf);
-      bf16x8 nq, nk;
+      unpack8<T>(qraw[kk], qf);
+      unpack8<T>(kraw[kk], kf);
+      V8 nq, nk;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) nq[j] = bf(qf[j] * iq), nk[j] = bf(kf[j] * ik);
+      for (int j = 0; j < 8; ++j) nq[j] = cv<T>(qf[j] * iq), nk[j] = cv<T>(kf[j] * ik);
       qraw[kk] = *reinterpret_cast<const uint4*>(&nq);
       kraw[kk] = *reinterpret_cast<const uint4*>(&nk);
     }
@@ -496,15 +499,18 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
 
   // ---- 3b. operands: Lq, Lk = (q, k) e^{B - a_{p-1}} (block-start anchor), Kap = k e^{a_p - B} (block-end
   // anchor); Q e^B (times the output scale) and K e^{B_end - B} to the record ----
-  bf16x8 lq[KS], lk[KS];
+  V8 lq[KS], lk[KS];
+  // f16 operands: the diagonal strip tile runs on bf16 operands formed here in fp32 (see step 4)
+  constexpr bool kWideDiag = kGate && __is_same(T, _Float16);
+  bf16x8 dq[kWideDiag ? KS : 1], dk[kWideDiag ? KS : 1], dkey[kWideDiag ? KS : 1];
   const uint32_t keep_bits = valid ? 0xffffffffu : 0u;
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {
     const int ch = 32 * kk + 8 * g4;
     float qf[8], kf[8];
-    unpack8(make_uint4(qraw[kk].x & keep_bits, qraw[kk].y & keep_bits, qraw[kk].z & keep_bits,
+    unpack8<T>(make_uint4(qraw[kk].x & keep_bits, qraw[kk].y & keep_bits, qraw[kk].z & keep_bits,
                        qraw[kk].w & keep_bits), qf);
-    unpack8(make_uint4(kraw[kk].x & keep_bits, kraw[kk].y & keep_bits, kraw[kk].z & keep_bits,
+    unpack8<T>(make_uint4(kraw[kk].x & keep_bits, kraw[kk].y & keep_bits, kraw[kk].z & keep_bits,
                        kraw[kk].w & keep_bits), kf);
     float tw[8], ep[8], et[8];
 #pragma unroll
@@ -522,7 +528,7 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
 #pragma unroll
       for (int j = 0; j < 8; ++j) tw[j] = ta[j], ep[j] = tb[j], et[j] = td[j];
     }
-    bf16x8 vq, vk, vkap, vkd, vkt, vqd;
+    V8 vq, vk, vkap, vkd, vkt, vqd;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float ell = 1.f, rho = 1.f;
@@ -531,29 +537,46 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
         rho = __builtin_amdgcn_exp2f(tw[j] - bl[kk][j]);
       }
       const float q1 = qf[j] * ell, k1 = kf[j] * ell, kp1 = kf[j] * rho;
-      vq[j] = bf(q1);
-      vk[j] = bf(k1);
-      vkap[j] = bf(kp1);
-      vkd[j] = bf(k1 * ep[j]);
-      vkt[j] = bf(kp1 * et[j]);
-      vqd[j] = bf(q1 * (ep[j] * a.scale));
+      vq[j] = cv<T>(q1);
+      vk[j] = cv<T>(k1);
+      vkap[j] = cv<T>(kp1);
+      vkd[j] = cv<T>(k1 * ep[j]);
+      vkt[j] = cv<T>(kp1 * et[j]);
+      vqd[j] = cv<T>(q1 * (ep[j] * a.scale));
+      if constexpr (kWideDiag) {  // q e^{B - a_{p-1}}, k e^{B - a_{p-1}} and k e^{a_{p-1} - B} (0 for a hot channel)
+        dq[kk][j] = bf(q1);
+        dk[kk][j] = bf(k1);
+        dkey[kk][j] = bf(-tw[j] > kHot ? 0.f : kf[j] * __builtin_amdgcn_exp2f(-bl[kk][j]));
+      }
     }
     lq[kk] = vq;
     lk[kk] = vk;
     const int ro = (16 * p + l16) * KP + ch;
-    *reinterpret_cast<bf16x8*>(kap + ro) = vkap;
-    if constexpr (kDelta) *reinterpret_cast<bf16x8*>(kd + ro) = vkd;
+    *reinterpret_cast<V8*>(kap + ro) = vkap;
+    if constexpr (kDelta) *reinterpret_cast<V8*>(kd + ro) = vkd;
     // scale Q e^B in the permuted channel order: this lane's channels 8 g4 .. 8 g4 + 7 of the group land as two
     // 4-channel pieces at positions pb and pb + 8
     const int pb = 32 * kk + 16 * (g4 & 1) + 4 * (g4 >> 1);
-    __bf16* qrec = reinterpret_cast<__bf16*>(rec + R::QD);
-    *reinterpret_cast<bf16x4*>(qrec + R::rk(16 * p + l16, pb)) = bf16x4{vqd[0], vqd[1], vqd[2], vqd[3]};
-    *reinterpret_cast<bf16x4*>(qrec + R::rk(16 * p + l16, pb + 8)) = bf16x4{vqd[4], vqd[5], vqd[6], vqd[7]};
-    *reinterpret_cast<bf16x8*>(reinterpret_cast<__bf16*>(rec + R::KT) + R::rk(16 * p + l16, ch)) = vkt;
+    T* qrec = reinterpret_cast<T*>(rec + R::QD);
+    *reinterpret_cast<V4*>(qrec + R::rk(16 * p + l16, pb)) = V4{vqd[0], vqd[1], vqd[2], vqd[3]};
+    *reinterpret_cast<V4*>(qrec + R::rk(16 * p + l16, pb + 8)) = V4{vqd[4], vqd[5], vqd[6], vqd[7]};
+    *reinterpret_cast<V8*>(reinterpret_cast<T*>(rec + R::KT) + R::rk(16 * p + l16, ch)) = vkt;
   }
   lds_barrier();
 
   // ---- 4. gated strips of block row p: tiles (p, j <= p) of Sc and P ----
+  // Off-diagonal key factors are <= 1.  The diagonal tile's e^{-T_p} is bounded only by the hot threshold (e^60):
+  // with f16 operands (range 65504, subnormal below 6e-5) the diagonal tile instead runs on the bf16 operands formed
+  // in fp32 in step 3b from this lane's own row (the diagonal tile's key rows are the lanes' own rows), the
+  // precision the bf16 path gives it; the f16 result of that tile is replaced by a select (every MFMA runs).
+  floatx4 diag_s = {0.f, 0.f, 0.f, 0.f}, diag_p = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (kWideDiag) {
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      diag_s = mfma32(dq[kk], dkey[kk], diag_s);
+      if constexpr (kDelta) diag_p = mfma32(dk[kk], dkey[kk], diag_p);
+    }
+  }
   for (int j = 0; j <= p; ++j) {
     floatx4 acc_s = {0.f, 0.f, 0.f, 0.f}, acc_p = {0.f, 0.f, 0.f, 0.f};
     const bool diag = j == p, adjacent = j + 1 == p;
@@ -561,25 +584,29 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       const int ch = 32 * kk + 8 * g4;
-      bf16x8 bk = *reinterpret_cast<const bf16x8*>(kap + (16 * j + l16) * KP + ch);
+      V8 bk = *reinterpret_cast<const V8*>(kap + (16 * j + l16) * KP + ch);
       if (kGate && !adjacent) {
         const float4 f0 = *reinterpret_cast<const float4*>(kscale + ch);
         const float4 f1 = *reinterpret_cast<const float4*>(kscale + ch + 4);
         const float f[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) bk[e] = bf(f32(bk[e]) * f[e]);
+        for (int e = 0; e < 8; ++e) bk[e] = cv<T>(f32(bk[e]) * f[e]);
       }
       acc_s = mfma32(lq[kk], bk, acc_s);
       if constexpr (kDelta) acc_p = mfma32(lk[kk], bk, acc_p);
     }
+    if constexpr (kWideDiag) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc_s[r] = diag ? diag_s[r] : acc_s[r], acc_p[r] = diag ? diag_p[r] : acc_p[r];
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 4 * g4 + r, sl = l16;
-      sct[tri_tile(p, j) * 256 + t * 16 + sl] = bf(diag && t < sl ? 0.f : acc_s[r]);
+      sct[tri_tile(p, j) * 256 + t * 16 + sl] = cv<T>(diag && t < sl ? 0.f : acc_s[r]);
       if constexpr (kDelta) {
         const float pv = acc_p[r] * sbeta[16 * p + t];
         if (diag) lii[p * 256 + t * 16 + sl] = t > sl ? pv : 0.f;
-        else negl[strict_tile(p, j) * 256 + t * 16 + sl] = bf(-pv);
+        else negl[strict_tile(p, j) * 256 + t * 16 + sl] = cv<T>(-pv);
       }
     }
   }
@@ -596,19 +623,20 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
         hot_diag_fixup<K, kDelta>(c * kChunk, p, len, hot_mask, sct + tri_tile(p, p) * 256, lii + p * 256,
                                   sbeta + 16 * p, rows);
       };
-      if (kPro && (kLowRank || kConv || (pro.flags & GDR_PRO_NORM_QK))) {
+      if constexpr (kPro != 0) {
+      if (kLowRank || kConv || (pro.flags & GDR_PRO_NORM_QK)) {
         // The fused prologue's inputs are not in memory as the kernel used them: q, k are renormalised with the
         // row norms kept in LDS, and the gate is recomputed from z and W (the R-long dot split over the 4 lanes
         // that share a row).
         const bool norm = pro.flags & GDR_PRO_NORM_QK;
         auto rows = [&](int tcr, int ch, float& q, float& k, float& g) {
-          InputRows{x, kGate}(tcr, ch, q, k, g);  // g is replaced below when it is computed
+          InputRowsT<T>{x, kGate}(tcr, ch, q, k, g);  // g is replaced below when it is computed
           if (conv) {
             q = conv4_silu1(x.qp + ch, x.q_st, tcr, cwq + ch * 4, state_rows(0, ck, int64_t(h) * K + ch));
             k = conv4_silu1(x.kp + ch, x.k_st, tcr, cwk + ch * 4, state_rows(1, ck, int64_t(h) * K + ch));
           }
           const int r = tcr - c * kChunk;          // row within the chunk (clamped rows stay inside it)
-          if (norm) q = f32(bf(q * snorm[r])), k = f32(bf(k * snorm[64 + r]));
+          if (norm) q = f32(cv<T>(q * snorm[r])), k = f32(cv<T>(k * snorm[64 + r]));
           if constexpr (kLowRank) {
             const int R = pro.rank, part = lane >> 4, span = R / 4;
             const __bf16* zr = static_cast<const __bf16*>(pro.gate_lowrank.ptr) + bidx * pro.gate_lowrank.stride_b +
@@ -617,8 +645,8 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
             float acc = 0.f;
             for (int e = 0; e < span; e += 8) {
               float zf[8], wf[8];
-              unpack8(*reinterpret_cast<const uint4*>(zr + e), zf);
-              unpack8(*reinterpret_cast<const uint4*>(wr + e), wf);
+              unpack8<__bf16>(*reinterpret_cast<const uint4*>(zr + e), zf);
+              unpack8<__bf16>(*reinterpret_cast<const uint4*>(wr + e), wf);
 #pragma unroll
               for (int j = 0; j < 8; ++j) acc += zf[j] * wf[j];
             }
@@ -630,7 +658,10 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
         };
         fixup(rows);
       } else {
-        fixup(InputRows{x, kGate});
+        fixup(InputRowsT<T>{x, kGate});
+      }
+      } else {
+        fixup(InputRowsT<T>{x, kGate});
       }
     }
   }
@@ -660,15 +691,15 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
         xcol[r] = acc0 + acc1;
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ainv[p * 256 + r * 16 + lane] = bf(xcol[r]);
+      for (int r = 0; r < 16; ++r) ainv[p * 256 + r * 16 + lane] = cv<T>(xcol[r]);
     }
   }
   stage_v_pass(0);
   for (int i = threadIdx.x; i < 10 * 256 / 8; i += 256) {
-    bf16x8 v8 = reinterpret_cast<const bf16x8*>(sct)[i];
+    V8 v8 = reinterpret_cast<const V8*>(sct)[i];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v8[e] = bf(f32(v8[e]) * a.scale);
-    reinterpret_cast<bf16x8*>(rec + R::SC)[i] = v8;
+    for (int e = 0; e < 8; ++e) v8[e] = cv<T>(f32(v8[e]) * a.scale);
+    reinterpret_cast<V8*>(rec + R::SC)[i] = v8;
   }
   lds_barrier();
 
@@ -677,15 +708,15 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
   // column l16) feeds the later blocks; for W the transposed product X_i^T = Y_i^T A_ii^T (the same two operands
   // with their roles swapped) puts four consecutive channels of one row in each lane for 8-byte row stores.  The
   // right-hand side comes from row-major LDS tiles through one transposing read per block. ----
-  __bf16* wrec = reinterpret_cast<__bf16*>(rec + R::W);
-  __bf16* utrec = reinterpret_cast<__bf16*>(rec + R::FIX);
+  T* wrec = reinterpret_cast<T*>(rec + R::W);
+  T* utrec = reinterpret_cast<T*>(rec + R::FIX);
   const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
   auto solve_tile = [&](int rhs_off, int col0, bool is_w, int out_col0) {
-    bf16x4 xs[4];
+    V4 xs[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int off = rhs_off + ((16 * i + 4 * g4 + (l16 >> 2)) * KP + col0 + 4 * (l16 & 3)) * 2;
-      const bf16x4 rv = lds_read_tr(smem, off);  // rows 16 i + 4 g4 + r, column col0 + l16
+      const V4 rv = lds_read_tr<T>(smem, off);  // rows 16 i + 4 g4 + r, column col0 + l16
       floatx4 z;
 #pragma unroll
       for (int r = 0; r < 4; ++r) z[r] = f32(rv[r]);
@@ -694,22 +725,22 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
         for (int r = 0; r < 4; ++r) z[r] *= sbeta[16 * i + 4 * g4 + r];
 #pragma unroll
         for (int j = 0; j < i; ++j) {
-          const bf16x4 nl = *reinterpret_cast<const bf16x4*>(negl + strict_tile(i, j) * 256 + l16 * 16 + 4 * g4);
+          const V4 nl = *reinterpret_cast<const V4*>(negl + strict_tile(i, j) * 256 + l16 * 16 + 4 * g4);
           z = mfma16(nl, xs[j], z);
         }
-        const bf16x4 ai = *reinterpret_cast<const bf16x4*>(ainv + i * 256 + l16 * 16 + 4 * g4);
-        const bf16x4 zb = pack4(z);
-        xs[i] = pack4(mfma16(ai, zb, zero4));
+        const V4 ai = *reinterpret_cast<const V4*>(ainv + i * 256 + l16 * 16 + 4 * g4);
+        const V4 zb = pack4<T>(z);
+        xs[i] = pack4<T>(mfma16(ai, zb, zero4));
         if (is_w) {
           // X_i^T: row 16 i + l16, channels out_col0 + 4 g4 + r, stored in the permuted channel order
-          const bf16x4 xt = pack4(mfma16(zb, ai, zero4));
+          const V4 xt = pack4<T>(mfma16(zb, ai, zero4));
           const int wpos = 32 * (out_col0 >> 5) + 8 * g4 + 4 * ((out_col0 >> 4) & 1);
-          *reinterpret_cast<bf16x4*>(wrec + R::rk(16 * i + l16, wpos)) = xt;
+          *reinterpret_cast<V4*>(wrec + R::rk(16 * i + l16, wpos)) = xt;
         }
       } else {
-        xs[i] = pack4(z);
+        xs[i] = pack4<T>(z);
       }
-      if (!is_w) *reinterpret_cast<bf16x4*>(utrec + R::rt(out_col0 + l16, 16 * i + 4 * g4)) = xs[i];
+      if (!is_w) *reinterpret_cast<V4*>(utrec + R::rt(out_col0 + l16, 16 * i + 4 * g4)) = xs[i];
     }
   };
   if constexpr (kDelta) {
@@ -728,14 +759,15 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
 
   // fused prologue: the last chunk of a sequence stores the last 3 inputs of each of its head's q, k, v channels,
   // reaching back into the state it was given when the sequence is shorter than 3
-  if (conv && (c + 1) * kChunk >= len) {
+  if constexpr (kConv) {
+  if ((c + 1) * kChunk >= len) {
     const int V = a.value_dim, nqk = 2 * K * 3, ntot = nqk + V * 3;
     for (int idx = threadIdx.x; idx < ntot; idx += 256) {
       const int i = idx < nqk ? idx / (K * 3) : 2;
       const int rem = idx < nqk ? idx % (K * 3) : idx - nqk, ch = rem / 3, sl = rem % 3;
       __bf16* so = static_cast<__bf16*>(pro.conv_state_out[i]);
       if (!so) continue;
-      const int64_t nch = i < 2 ? ck : cv;
+      const int64_t nch = i < 2 ? ck : cvv;
       const int64_t row = int64_t(n) * nch + (i < 2 ? int64_t(h) * K : int64_t(h) * V) + ch;
       const int r = len - 3 + sl;
       __bf16 val;
@@ -749,6 +781,7 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
       }
       so[row * 3 + sl] = val;
     }
+  }
   }
 }
 
@@ -766,7 +799,7 @@ struct ScanShape {
 
 // kStates (backward recompute): instead of the output, write the fp32 state entering every chunk (and the final
 // one) to `states` [NC + 1][K][V] and the bf16 u to `ubuf` [NC * 64][V], per (sequence, head).
-template <int VARIANT, int K, typename OutT, int SL, int NT, bool kStates = false>
+template <int VARIANT, int K, typename OutT, int SL, int NT, bool kStates = false, typename T = __bf16>
 __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_kernel(const gdr_args a, int n_slices,
                                                                                 int xcd_map, int nc,
                                                                                 int64_t rec_bytes,
@@ -774,6 +807,8 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
                                                                                 __bf16* __restrict__ ubuf) {
   constexpr bool kDelta = VARIANT != GDR_GLA;
   constexpr int KT = K / 16, KS = K / 32;
+  using V8 = vec8<T>;
+  using V4 = vec4<T>;
   constexpr int kScanCompute = ScanShape<SL, NT>::kCompute, kOP = ScanShape<SL, NT>::kOP;
   constexpr int kScanLoaders = ScanShape<SL, NT>::kLoaders;
   using R = Rec<K>;
@@ -894,38 +929,38 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
   for (int s = 0; s < nchunks; ++s) {
     const unsigned char* bb = smem + (s & 1) * SB;
     if constexpr (kStates) store_state(s);
-    const __bf16* wl = reinterpret_cast<const __bf16*>(bb + R::W);
-    const __bf16* ql = reinterpret_cast<const __bf16*>(bb + R::QD);
-    const __bf16* scl = reinterpret_cast<const __bf16*>(bb + R::SC);
+    const T* wl = reinterpret_cast<const T*>(bb + R::W);
+    const T* ql = reinterpret_cast<const T*>(bb + R::QD);
+    const T* scl = reinterpret_cast<const T*>(bb + R::SC);
     const float* gam = reinterpret_cast<const float*>(bb + R::GAM);
-    const __bf16* utl = reinterpret_cast<const __bf16*>(bb + R::FIX);  // UT rows of this slice
+    const T* utl = reinterpret_cast<const T*>(bb + R::FIX);  // UT rows of this slice
 
     // Every LDS read of the step is issued ahead of its use, in the order of use (LDS reads return in order):
     // W / Q e^B fragments one row block ahead, the U rows with the first block, the score tiles and the first two
     // K e^{B_end - B} tiles (with their gamma) during the last block, each further Kt tile two tiles ahead.
 
     // state as the bf16 B operand: two accumulator tiles = one 32-deep k slot set {32kk + 4g4 + r, +16}
-    bf16x8 sB[NT][KS];
+    V8 sB[NT][KS];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) sB[t][kk] = concat(pack4(st[t][2 * kk]), pack4(st[t][2 * kk + 1]));
+      for (int kk = 0; kk < KS; ++kk) sB[t][kk] = concat(pack4<T>(st[t][2 * kk]), pack4<T>(st[t][2 * kk + 1]));
 
     // X = W S (accumulator layout: token rows, state columns) and the transposed readout (Q e^B S)^T = S^T (Q e^B)^T
     // (the same operands with their roles swapped: state-column rows, token columns), so that each lane ends up
     // with four consecutive output columns of one token.  Every A fragment read from LDS feeds NT tiles.
     floatx4 acc_ot[NT][4];
-    bf16x4 ub[NT][4];
-    bf16x8 fq[2][KS], fw[2][KS];  // A fragments of row block i (k slots {32kk + 4g4 + r, +16})
+    V4 ub[NT][4];
+    V8 fq[2][KS], fw[2][KS];  // A fragments of row block i (k slots {32kk + 4g4 + r, +16})
     auto read_block = [&](int i, int buf) {
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
         const int r0 = R::rk(16 * i + l16, 32 * kk + 8 * g4);  // permuted order: one 16-byte read
-        if constexpr (!kStates) fq[buf][kk] = *reinterpret_cast<const bf16x8*>(ql + r0);
-        if constexpr (kDelta) fw[buf][kk] = *reinterpret_cast<const bf16x8*>(wl + r0);
+        if constexpr (!kStates) fq[buf][kk] = *reinterpret_cast<const V8*>(ql + r0);
+        if constexpr (kDelta) fw[buf][kk] = *reinterpret_cast<const V8*>(wl + r0);
       }
     };
-    bf16x8 fk[3][2];  // Kt^T fragments of state tile m (transposing reads of the row-major tile), ring of 3
+    V8 fk[3][2];  // Kt^T fragments of state tile m (transposing reads of the row-major tile), ring of 3
     float4 gm[3];     // gamma of the same rows
     auto read_kt = [&](int m) {
       const int buf = m % 3;
@@ -934,19 +969,19 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
         const int tok = 32 * kk + 4 * g4 + (l16 >> 2);
         const int chn = 16 * m + 4 * (l16 & 3);
         const int off = (s & 1) * SB + R::KT;
-        fk[buf][kk] = concat(lds_read_tr(smem, off + R::rk(tok, chn) * 2),
-                             lds_read_tr(smem, off + R::rk(tok + 16, chn) * 2));
+        fk[buf][kk] = concat(lds_read_tr<T>(smem, off + R::rk(tok, chn) * 2),
+                             lds_read_tr<T>(smem, off + R::rk(tok + 16, chn) * 2));
       }
       gm[buf] = *reinterpret_cast<const float4*>(gam + 16 * m + 4 * g4);
     };
-    bf16x4 fsc[10];
+    V4 fsc[10];
     read_block(0, 0);
-    bf16x4 uu[NT][4];
+    V4 uu[NT][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        uu[t][i] = *reinterpret_cast<const bf16x4*>(utl + R::rt(c0 - v0 + 16 * t + l16, 16 * i + 4 * g4));
+        uu[t][i] = *reinterpret_cast<const V4*>(utl + R::rt(c0 - v0 + 16 * t + l16, 16 * i + 4 * g4));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (i + 1 < 4) {
@@ -954,7 +989,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
       } else {
         if constexpr (!kStates) {
 #pragma unroll
-          for (int q = 0; q < 10; ++q) fsc[q] = *reinterpret_cast<const bf16x4*>(scl + q * 256 + l16 * 16 + 4 * g4);
+          for (int q = 0; q < 10; ++q) fsc[q] = *reinterpret_cast<const V4*>(scl + q * 256 + l16 * 16 + 4 * g4);
         }
         read_kt(0);
         read_kt(1);
@@ -976,7 +1011,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
         floatx4 u;
 #pragma unroll
         for (int r = 0; r < 4; ++r) u[r] = kDelta ? f32(uu[t][i][r]) - ax[t][r] : f32(uu[t][i][r]);
-        ub[t][i] = pack4(u);
+        ub[t][i] = pack4<T>(u);
         acc_ot[t][i] = ao[t];
         if constexpr (kStates) {
 #pragma unroll
@@ -990,7 +1025,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
     // Sc_ij give B in the same order (a block past i contributes zeros).  Every MFMA accumulating onto the readout
     // has the readout's shape, so no accumulator passes between MFMAs of different shapes.
     if constexpr (!kStates) {
-      const bf16x4 z4 = {};
+      const V4 z4 = {};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1045,15 +1080,15 @@ int64_t slots_per_head(const gdr_args& a) {
   return int64_t(a.batch) * ((a.seq_len + kChunk - 1) / kChunk);
 }
 
-template <int VARIANT, int K, int kPro>
+template <int VARIANT, int K, int kPro, typename T = __bf16>
 hipError_t launch_prep(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
   const int nc = (a.seq_len + kChunk - 1) / kChunk;
   const int64_t n_prep = slots_per_head(a) * a.heads;
   constexpr int prep_lds = PrepLds<K>::BYTES;
-  hipError_t e = configure_lds<&chunk_prep_kernel<VARIANT, K, kPro>>(prep_lds);
+  hipError_t e = configure_lds<&chunk_prep_kernel<VARIANT, K, kPro, T>>(prep_lds);
   if (e != hipSuccess) return e;
   if (n_prep > 0)
-    hipLaunchKernelGGL((chunk_prep_kernel<VARIANT, K, kPro>), dim3(unsigned(n_prep)), dim3(256), prep_lds, stream,
+    hipLaunchKernelGGL((chunk_prep_kernel<VARIANT, K, kPro, T>), dim3(unsigned(n_prep)), dim3(256), prep_lds, stream,
                        a, nc, Rec<K>::bytes(a.value_dim), pro);
   return hipGetLastError();
 }
@@ -1081,12 +1116,12 @@ int scan_slice(int64_t bh, int value_dim) {
   return 16;
 }
 
-template <int VARIANT, int K, typename OutT, int SL, int NT, bool kStates>
+template <int VARIANT, int K, typename OutT, int SL, int NT, bool kStates, typename T>
 hipError_t launch_scan_sl(const gdr_args& a, int nc, float* states, __bf16* ubuf, hipStream_t stream) {
   using Sh = ScanShape<SL, NT>;
   constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::ut_slice(SL)) + (kStates ? 0 : 2 * 64 * Sh::kOP * int(sizeof(OutT)));
   static_assert(scan_lds <= 160 * 1024, "scan LDS");
-  constexpr auto kernel = &chunk_scan_kernel<VARIANT, K, OutT, SL, NT, kStates>;
+  constexpr auto kernel = &chunk_scan_kernel<VARIANT, K, OutT, SL, NT, kStates, T>;
   hipError_t e = configure_lds<kernel>(scan_lds);
   if (e != hipSuccess) return e;
   const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
@@ -1098,19 +1133,24 @@ hipError_t launch_scan_sl(const gdr_args& a, int nc, float* states, __bf16* ubuf
   return hipGetLastError();
 }
 
-template <int VARIANT, int K, typename OutT, bool kStates>
+template <int VARIANT, int K, typename OutT, bool kStates, typename T = __bf16>
 hipError_t launch_scan(const gdr_args& a, float* states, __bf16* ubuf, hipStream_t stream) {
   const int nc = (a.seq_len + kChunk - 1) / kChunk;
   const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
   switch (scan_slice(int64_t(n_seq) * a.heads, a.value_dim)) {
-    case 64: return launch_scan_sl<VARIANT, K, OutT, 64, 1, kStates>(a, nc, states, ubuf, stream);
-    case 32: return launch_scan_sl<VARIANT, K, OutT, 32, 1, kStates>(a, nc, states, ubuf, stream);
-    default: return launch_scan_sl<VARIANT, K, OutT, 16, 1, kStates>(a, nc, states, ubuf, stream);
+    case 64: return launch_scan_sl<VARIANT, K, OutT, 64, 1, kStates, T>(a, nc, states, ubuf, stream);
+    case 32: return launch_scan_sl<VARIANT, K, OutT, 32, 1, kStates, T>(a, nc, states, ubuf, stream);
+    default: return launch_scan_sl<VARIANT, K, OutT, 16, 1, kStates, T>(a, nc, states, ubuf, stream);
   }
 }
 
 template <int VARIANT, int K, typename OutT>
 hipError_t launch_split_typed(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
+  if (a.q.dtype == GDR_F16) {  // f16 q, k, v: f16 MFMA operands and records (plain op only)
+    hipError_t e = launch_prep<VARIANT, K, 0, _Float16>(a, pro, stream);
+    if (e != hipSuccess) return e;
+    return launch_scan<VARIANT, K, OutT, false, _Float16>(a, nullptr, nullptr, stream);
+  }
   hipError_t e;
   const bool conv = pro.flags & GDR_PRO_CONV;
   if (!pro.flags) {

@@ -165,9 +165,14 @@ int chunk_fwd(const gdr_args* a, const gdr_prologue* pro, hipStream_t stream) {
   const bool lowrank = pro && (pro->flags & GDR_PRO_GATE_LOWRANK);
   if ((rc = check_common(a, true, true, !lowrank))) return rc;
   if (pro && !a->workspace) return fail(GDR_ERR_INVALID, "the fused prologue needs a workspace (two-launch path)");
-  if (a->q.dtype != GDR_BF16 || a->k.dtype != GDR_BF16 || a->v.dtype != GDR_BF16)
-    return fail(GDR_ERR_UNSUPPORTED, "chunk mode reads bf16 q, k, v (got dtype codes %d, %d, %d)", a->q.dtype,
-                a->k.dtype, a->v.dtype);
+  // q, k, v are the MFMA operands' type: all bf16, or all f16 (the two-launch path of the plain op).
+  const bool f16 = a->q.dtype == GDR_F16 && a->k.dtype == GDR_F16 && a->v.dtype == GDR_F16;
+  if (!f16 && (a->q.dtype != GDR_BF16 || a->k.dtype != GDR_BF16 || a->v.dtype != GDR_BF16))
+    return fail(GDR_ERR_UNSUPPORTED, "chunk mode reads q, k, v of one 16-bit type, bf16 or f16 (got dtype codes %d, "
+                "%d, %d); the recurrent mode takes f32", a->q.dtype, a->k.dtype, a->v.dtype);
+  if (f16 && (pro || !a->workspace))
+    return fail(GDR_ERR_UNSUPPORTED, "f16 q, k, v run on the two-launch path of the plain op only (a workspace, no "
+                "fused prologue)");
   // Rows of q, k, v, gate and out are moved with 16-byte accesses.
   const gdr_tensor* rows[] = {&a->q, &a->k, &a->v, &a->out, &a->gate};
   const char* names[] = {"query", "key", "value", "out", "gate"};
@@ -444,7 +449,7 @@ int gdr_chunk_bwd(const gdr_args* a, const gdr_grads* g, void* workspace, int64_
   if (!g) return fail(GDR_ERR_INVALID, "grads is NULL");
   if (a->cu_seqlens) return fail(GDR_ERR_UNSUPPORTED, "the chunk backward does not take packed varlen input");
   if (a->q.dtype != GDR_BF16 || a->k.dtype != GDR_BF16 || a->v.dtype != GDR_BF16)
-    return fail(GDR_ERR_UNSUPPORTED, "chunk mode reads bf16 q, k, v (got dtype codes %d, %d, %d)", a->q.dtype,
+    return fail(GDR_ERR_UNSUPPORTED, "the chunk backward reads bf16 q, k, v (got dtype codes %d, %d, %d)", a->q.dtype,
                 a->k.dtype, a->v.dtype);
   const bool has_gate = a->variant != GDR_DELTANET, has_beta = a->variant != GDR_GLA;
   if ((rc = check_view(g->d_out, "d_out", true, false))) return rc;

@@ -4,7 +4,7 @@ against autograd of the fp64 oracle on the same bf16-rounded inputs.
 Mirrors the reference's gradient check (src tests/test_kimi_delta_attention.py:46-53: loss = sum(out * grad_out)
 plus a final-state term, gradients for q, k, v, gate, beta and the initial state) over its grid of shapes and gate
 strengths (:107-114), for all four variants, plus the layer's transposed layout, partial requires_grad, an absent
-initial state, an fp32 value dtype and a longer sequence.
+initial state and a longer sequence; fp32 values (which run the fp32 recurrence) are refused with a clear error.
 
 Tolerance: max|d - d_ref| <= 2e-2 * max|d_ref| for dq, dk, dv, dbeta and d(initial state); 3e-2 for the gate
 gradient, a reverse cumulative sum over each chunk of terms that each carry bf16 operand rounding.
@@ -135,7 +135,14 @@ def test_chunk_backward_without_initial_or_final_state():
     _check("gdn", inp, "gdn no h0, no final-state gradient", with_final=False)
 
 
-def test_chunk_backward_fp32_values_and_long_sequence():
+def test_chunk_backward_long_sequence():
     inp = workloads.make_inputs("kda", 1, 1024, 2, 128, 128, seed=6, gate_scale=4.0, state_std=1.0)
-    inp.value = inp.value.float()  # the op casts q, k, v to bf16 and returns an fp32 output
-    _check("kda", inp, "kda fp32 value, T=1024")
+    _check("kda", inp, "kda T=1024")
+
+
+def test_chunk_backward_refuses_fp32_values():
+    """An fp32 value makes the op run the fp32 recurrence (no rounding to bf16), which has no backward."""
+    inp = workloads.make_inputs("kda", 1, 64, 2, 64, 64, seed=6, device="cuda")
+    v = inp.value.float().requires_grad_()
+    with pytest.raises(NotImplementedError, match="fp32"):
+        CHUNK_FNS["kda"](inp.query, inp.key, v, inp.gate, inp.beta)
