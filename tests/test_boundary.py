@@ -363,3 +363,26 @@ def test_norm_gate_and_fused_conv_refuse_cpu_tensors():
     cw = [torch.randn(128, 1, 4)] * 3
     with pytest.raises(ValueError, match="GPU"):
         gdr.chunk_kimi_delta_attention_fused(q, k, v, z, w, None, a_log, b, conv_weights=cw)
+
+
+def test_integration_stub_builds_args_the_library_accepts():
+    """The ctypes stub in INTEGRATION.md (its definitions, up to the usage marker) builds a gdr_args that the built
+    library accepts: gdr_chunk_workspace_bytes (no pointer is dereferenced, so CPU tensors serve) returns the same
+    byte count as this package's own binding, for bf16 and for f16 inputs."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    start = text.index("A minimal ctypes stub")
+    block = text[text.index("```python\n", start) + len("```python\n"):]
+    block = block[:block.index("# --- usage")]
+    block = block.replace('"gtar-kimik3-public_amd/libgdr.so"', repr(lib.LIBRARY_PATH))
+    ns = {}
+    exec(compile(block, "INTEGRATION.md stub", "exec"), ns)
+    B, H, T, K, V = 2, 4, 200, 128, 128
+    for dtype in (torch.bfloat16, torch.float16):
+        q, k = torch.zeros(B, H, T, K, dtype=dtype), torch.zeros(B, H, T, K, dtype=dtype)
+        v, o = torch.zeros(B, H, T, V, dtype=dtype), torch.zeros(B, H, T, V, dtype=dtype)
+        g, beta = torch.zeros(B, H, T, K), torch.zeros(B, H, T)
+        a = ns["chunk_args"](q, k, v, g, beta, o)
+        got = ns["lib"].gdr_chunk_workspace_bytes(ctypes.byref(a))
+        own = lib.make_args(lib.KDA, q, k, v, g, beta, o, K ** -0.5, None, None)
+        want = lib.load_library().gdr_chunk_workspace_bytes(ctypes.byref(own))
+        assert got == want > 0, (got, want, ns["lib"].gdr_last_error())
