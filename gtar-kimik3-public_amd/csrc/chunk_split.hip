@@ -960,10 +960,10 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
         if constexpr (kDelta) fw[buf][kk] = *reinterpret_cast<const V8*>(wl + r0);
       }
     };
-    V8 fk[3][2];  // Kt^T fragments of state tile m (transposing reads of the row-major tile), ring of 3
-    float4 gm[3];     // gamma of the same rows
+    V8 fk[4][2];    // Kt^T fragments of state tile m (transposing reads of the row-major tile), ring of 4
+    float4 gm[4];   // gamma of the same rows
     auto read_kt = [&](int m) {
-      const int buf = m % 3;
+      const int buf = m % 4;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const int tok = 32 * kk + 4 * g4 + (l16 >> 2);
@@ -1037,22 +1037,27 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
                                   concat(fsc[tri_tile(i, j)], pair ? fsc[tri_tile(i, j + 1)] : z4), acc_ot[t][i]);
           }
     }
-    // S = diag(gamma) S + Kt^T u
+    // S = diag(gamma) S + Kt^T u.  Each state tile takes two dependent MFMAs (tokens 0-31, then 32-63); they are
+    // software-pipelined across tiles (tile m's first beside tile m-1's second), so consecutive MFMAs never depend on
+    // each other and each tile's accumulation order is unchanged.
+    auto update_half = [&](int m, int kk) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        st[t][m] = mfma32(fk[m % 4][kk], concat(ub[t][2 * kk], ub[t][2 * kk + 1]), st[t][m]);
+    };
 #pragma unroll
     for (int m = 0; m < KT; ++m) {
       if (m + 2 < KT) read_kt(m + 2);
       __builtin_amdgcn_sched_barrier(0);
-      const float4 g = gm[m % 3];
+      const float4 g = gm[m % 4];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         st[t][m][0] *= g.x; st[t][m][1] *= g.y; st[t][m][2] *= g.z; st[t][m][3] *= g.w;
       }
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-          st[t][m] = mfma32(fk[m % 3][kk], concat(ub[t][2 * kk], ub[t][2 * kk + 1]), st[t][m]);
+      update_half(m, 0);
+      if (m > 0) update_half(m - 1, 1);
     }
+    update_half(KT - 1, 1);
     // output: lane holds O[token 16 i + l16][columns c0 + 16 t + 4 g4 .. + 3], into the chunk's LDS tile
     if constexpr (!kStates) {
       OutT* tw = otile + (s & 1) * 64 * kOP;
