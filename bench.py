@@ -469,7 +469,14 @@ def bench_train(gdr, workloads, torch, steps, warmup):
     def forward():
         return gdr.chunk_kimi_delta_attention(*leaves[:5], initial_state=leaves[5], output_final_state=True)
 
+    def clear_grads():
+        # the gradients are written fresh each step (autograd would otherwise add them into .grad, which is
+        # PyTorch's accumulation, not the op's backward)
+        for x in leaves:
+            x.grad = None
+
     def step():
+        clear_grads()
         out, final = forward()
         torch.autograd.backward([out, final], [d_out, d_final])
 
@@ -480,6 +487,7 @@ def bench_train(gdr, workloads, torch, steps, warmup):
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     fwd_ms, tot_ms = 0.0, 0.0
     for _ in range(steps):
+        clear_grads()
         ev[0].record(stream)
         out, final = forward()
         ev[1].record(stream)

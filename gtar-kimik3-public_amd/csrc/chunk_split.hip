@@ -797,13 +797,13 @@ struct ScanShape {
   static constexpr int kOP = SL + 8;                             // row pitch (elements) of the output tile in LDS
 };
 
-// kStates (backward recompute): instead of the output, write the fp32 state entering every chunk (and the final
-// one) to `states` [NC + 1][K][V] and the bf16 u to `ubuf` [NC * 64][V], per (sequence, head).
+// kStates (backward recompute): instead of the output, write the state entering every chunk to `states` [NC][K][V]
+// (bf16, rounded as the MFMA operand) and the bf16 u to `ubuf` [NC * 64][V], per (sequence, head).
 template <int VARIANT, int K, typename OutT, int SL, int NT, bool kStates = false, typename T = __bf16>
 __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_kernel(const gdr_args a, int n_slices,
                                                                                 int xcd_map, int nc,
                                                                                 int64_t rec_bytes,
-                                                                                float* __restrict__ states,
+                                                                                __bf16* __restrict__ states,
                                                                                 __bf16* __restrict__ ubuf) {
   constexpr bool kDelta = VARIANT != GDR_GLA;
   constexpr int KT = K / 16, KS = K / 32;
@@ -913,7 +913,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
   lds_barrier();
 
   const int V = a.value_dim;
-  const size_t st_base = size_t(n * H + h) * (nc + 1) * K * V;  // kStates buffers (non-varlen only)
+  const size_t st_base = size_t(n * H + h) * nc * K * V;  // kStates buffers (non-varlen only)
   const size_t ub_base = size_t(n * H + h) * nc * kChunk * V;
   auto store_state = [&](int c) {
 #pragma unroll
@@ -922,7 +922,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
       for (int m = 0; m < KT; ++m)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          states[st_base + (size_t(c) * K + 16 * m + 4 * g4 + r) * V + c0 + 16 * t + l16] = st[t][m][r];
+          states[st_base + (size_t(c) * K + 16 * m + 4 * g4 + r) * V + c0 + 16 * t + l16] = bf(st[t][m][r]);
   };
 
   OutT* otile = reinterpret_cast<OutT*>(smem + 2 * SB);
@@ -1068,7 +1068,6 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
     }
     lds_barrier();
   }
-  if constexpr (kStates) store_state(nchunks);
   if (a.ht) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -1122,7 +1121,7 @@ int scan_slice(int64_t bh, int value_dim) {
 }
 
 template <int VARIANT, int K, typename OutT, int SL, int NT, bool kStates, typename T>
-hipError_t launch_scan_sl(const gdr_args& a, int nc, float* states, __bf16* ubuf, hipStream_t stream) {
+hipError_t launch_scan_sl(const gdr_args& a, int nc, __bf16* states, __bf16* ubuf, hipStream_t stream) {
   using Sh = ScanShape<SL, NT>;
   constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::ut_slice(SL)) + (kStates ? 0 : 2 * 64 * Sh::kOP * int(sizeof(OutT)));
   static_assert(scan_lds <= 160 * 1024, "scan LDS");
@@ -1139,7 +1138,7 @@ hipError_t launch_scan_sl(const gdr_args& a, int nc, float* states, __bf16* ubuf
 }
 
 template <int VARIANT, int K, typename OutT, bool kStates, typename T = __bf16>
-hipError_t launch_scan(const gdr_args& a, float* states, __bf16* ubuf, hipStream_t stream) {
+hipError_t launch_scan(const gdr_args& a, __bf16* states, __bf16* ubuf, hipStream_t stream) {
   const int nc = (a.seq_len + kChunk - 1) / kChunk;
   const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
   switch (scan_slice(int64_t(n_seq) * a.heads, a.value_dim)) {
@@ -1194,7 +1193,7 @@ hipError_t launch_states_typed(const gdr_args& fwd, const BwdLayout& L, unsigned
   a.ht = nullptr;
   hipError_t e = launch_prep<VARIANT, K, 0>(a, gdr_prologue{}, stream);
   if (e != hipSuccess) return e;
-  return launch_scan<VARIANT, K, __bf16, true>(a, reinterpret_cast<float*>(ws + L.states),
+  return launch_scan<VARIANT, K, __bf16, true>(a, reinterpret_cast<__bf16*>(ws + L.states),
                                               reinterpret_cast<__bf16*>(ws + L.ubuf), stream);
 }
 

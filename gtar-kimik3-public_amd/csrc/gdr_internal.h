@@ -47,17 +47,15 @@ hipError_t launch_norm_gate(const gdr_norm_gate_args& a, hipStream_t stream);
 int64_t chunk_workspace_bytes(const gdr_args& a);
 hipError_t launch_chunk_split(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream);
 
-// Byte offsets of the chunkwise-backward buffers inside its workspace (each 256-aligned).  Per (sequence, head):
-//   rec      the forward records (chunk_workspace_bytes layout)
-//   states   fp32 [NC + 1][K][V]  state entering each chunk (the last one is the final state)
-//   dstates  fp32 [NC + 1][K][V]  gradient of each of those states
-//   ubuf     bf16 [NC * 64][V]    u = U - W S per chunk row
-//   dubuf    bf16 [NC * 64][V]    its gradient
-//   dqd, dw, dkt  fp32 [NC * 64][K]  dO S^T, -du S^T, u dS'^T per chunk
-//   dsc      fp32 [NC][64][64]   tril(dO u^T) per chunk
-//   bnd      fp32 [NC][K]        rowsum(S (x) dS') per chunk (S entering it, dS' leaving it)
+// Byte offsets of the chunkwise-backward buffers inside its workspace (each 256-aligned).  Per (sequence, head,
+// chunk):
+//   rec      the forward record (chunk_workspace_bytes layout)
+//   states   bf16 [K][V]   the state entering the chunk
+//   dstates  bf16 [K][V]   the gradient of the state leaving it
+//   ubuf     bf16 [64][V]  u = U - W S of the chunk's rows
+//   dubt     bf16 [V][64]  its gradient, transposed
 struct BwdLayout {
-  int64_t rec, states, dstates, ubuf, dubuf, dqd, dw, dkt, dsc, bnd, total;
+  int64_t rec, states, dstates, ubuf, dubt, total;
 };
 BwdLayout chunk_bwd_layout(const gdr_args& a);
 
