@@ -12,8 +12,11 @@ gated_deltanet.py:472-520, gated_linear_attention.py:437-483, deltanet.py:399-44
   * the output has the value's dtype; `(out, final_state)` is returned only when `output_final_state`.
 The chunk ops are differentiable like the reference's torch.autograd.Function classes
 (kimi_delta_attention.py:534-622 and its twins): when an input requires grad, the forward runs through
-`_ChunkFunction`, whose backward is libgdr's gdr_chunk_bwd, returning gradients for q, k, v, gate, beta and the
-initial state (none for `scale`).
+`_ChunkFunction`, returning gradients for q, k, v, gate, beta and the initial state (none for `scale`).  Its
+forward is gdr_chunk_fwd_train, which also keeps the forward records, the per-chunk states and u in the backward
+workspace, and its backward is gdr_chunk_bwd_saved on that workspace.  The reference's backward recomputes the
+states instead (:566-571); with GDR_CHUNK_BWD_RECOMPUTE=1 in the environment this module does the same (plain
+forward, gdr_chunk_bwd), holding less memory between forward and backward.
 Differences, all deliberate: CPU tensors raise (the reference's CPU token loop is this repository's test oracle,
 not a product path); gradients through the recurrent ops raise (the reference's recurrent ops have none either)
 and so do gradients of packed varlen calls; packed variable-length input is accepted through `cu_seqlens` (the
@@ -21,6 +24,8 @@ reference has none).
 """
 
 from __future__ import annotations
+
+import os
 
 import torch
 
@@ -174,9 +179,10 @@ def _exact_f32(variant, query, key, value, gate, beta, scale, initial_state, out
 
 
 class _ChunkFunction(torch.autograd.Function):
-    """Chunk forward + gdr_chunk_bwd.  Inputs arrive resolved by `run`: bf16 q, k, v with 16-byte rows, fp32
-    gate / beta, fp32 contiguous initial state (or None).  Saves the inputs only; the backward recomputes the
-    per-chunk states, as the reference's backward does (kimi_delta_attention.py:555, :566-571)."""
+    """Chunk forward + backward.  Inputs arrive resolved by `run`: bf16 q, k, v with 16-byte rows, fp32 gate / beta,
+    fp32 contiguous initial state (or None).  The forward keeps the backward workspace it filled (records, states,
+    u) unless GDR_CHUNK_BWD_RECOMPUTE=1, in which case the backward recomputes them from the saved inputs as the
+    reference's does (kimi_delta_attention.py:555, :566-571)."""
 
     @staticmethod
     def forward(ctx, variant, query, key, value, gate, beta, scale, initial_state, out_dtype):
@@ -186,8 +192,13 @@ class _ChunkFunction(torch.autograd.Function):
         out = torch.empty(batch, heads, seq_len, value_dim, device=device, dtype=out_dtype)
         final_state = torch.empty(batch, heads, key_dim, value_dim, device=device, dtype=torch.float32)
         args = _lib.make_args(variant, query, key, value, gate, beta, out, scale, initial_state, final_state)
-        workspace = _lib.chunk_workspace(args, device)  # noqa: F841 (alive until enqueued)
-        _lib.launch("gdr_chunk_fwd", args, device)
+        if os.environ.get("GDR_CHUNK_BWD_RECOMPUTE", "0") == "1":
+            ctx.saved_ws = None
+            workspace = _lib.chunk_workspace(args, device)  # noqa: F841 (alive until enqueued)
+            _lib.launch("gdr_chunk_fwd", args, device)
+        else:
+            ctx.saved_ws = _lib.bwd_workspace(args, device)
+            _lib.chunk_forward_train(args, ctx.saved_ws, device)
         ctx.save_for_backward(query, key, value, gate, beta, initial_state)
         ctx.variant, ctx.scale = variant, scale
         return out, final_state
@@ -207,5 +218,7 @@ class _ChunkFunction(torch.autograd.Function):
         dh0 = torch.empty_like(initial_state) if initial_state is not None else None
         args = _lib.make_args(ctx.variant, query, key, value, gate, beta, None, ctx.scale, initial_state, None)
         grads = _lib.make_grads(d_out, d_final, dq, dk, dv, dg, db, dh0)
-        _lib.chunk_backward(args, grads, device)
+        # the saved workspace serves one backward; a second one (retain_graph) recomputes from the saved inputs
+        saved, ctx.saved_ws = ctx.saved_ws, None
+        _lib.chunk_backward(args, grads, device, saved)
         return None, dq, dk, dv, dg, db, None, dh0, None

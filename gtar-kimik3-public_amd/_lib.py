@@ -151,6 +151,10 @@ EXPORTS = {
     "gdr_chunk_bwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.POINTER(GdrGrads), ctypes.c_void_p,
                                      ctypes.c_int64, ctypes.c_void_p]),
     "gdr_chunk_bwd_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(GdrArgs)]),
+    "gdr_chunk_bwd_saved": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.POINTER(GdrGrads), ctypes.c_void_p,
+                                           ctypes.c_int64, ctypes.c_void_p]),
+    "gdr_chunk_fwd_train": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_int64,
+                                           ctypes.c_void_p]),
     "gdr_chunk_fwd": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
     "gdr_chunk_fwd_fused": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.POINTER(GdrPrologue), ctypes.c_void_p]),
     "gdr_chunk_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p]),
@@ -263,19 +267,38 @@ def make_grads(d_out, d_final, d_query, d_key, d_value, d_gate, d_beta, d_initia
     return grads
 
 
-def chunk_backward(args: GdrArgs, grads: GdrGrads, device: torch.device) -> None:
-    """Allocate the backward workspace from torch's caching allocator and enqueue gdr_chunk_bwd on torch's current
-    stream (the workspace tensor is released to the allocator, which orders reuse on that stream)."""
+def bwd_workspace(args: GdrArgs, device: torch.device) -> torch.Tensor:
+    """The chunk backward's workspace (gdr_chunk_bwd_workspace_bytes) from torch's caching allocator."""
     lib = load_library()
     nbytes = lib.gdr_chunk_bwd_workspace_bytes(ctypes.byref(args))
     if nbytes < 0:
         raise RuntimeError(f"gdr_chunk_bwd_workspace_bytes failed ({nbytes}): {lib.gdr_last_error().decode()}")
-    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def chunk_forward_train(args: GdrArgs, ws: torch.Tensor, device: torch.device) -> None:
+    """Enqueue gdr_chunk_fwd_train: the forward's out / ht, and in `ws` what gdr_chunk_bwd_saved reads."""
+    lib = load_library()
     stream = torch.cuda.current_stream(device).cuda_stream
+    _check("gdr_chunk_fwd_train", lib.gdr_chunk_fwd_train(ctypes.byref(args), ctypes.c_void_p(ws.data_ptr()),
+                                                          ctypes.c_int64(ws.numel()), ctypes.c_void_p(stream)))
+
+
+def chunk_backward(args: GdrArgs, grads: GdrGrads, device: torch.device, saved: torch.Tensor | None = None) -> None:
+    """Enqueue the chunk backward on torch's current stream: gdr_chunk_bwd_saved on `saved` (the workspace a
+    gdr_chunk_fwd_train of the same args filled), else gdr_chunk_bwd on a fresh workspace (released to the
+    allocator, which orders its reuse on that stream)."""
+    lib = load_library()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    if saved is not None:
+        rc = lib.gdr_chunk_bwd_saved(ctypes.byref(args), ctypes.byref(grads), ctypes.c_void_p(saved.data_ptr()),
+                                     ctypes.c_int64(saved.numel()), ctypes.c_void_p(stream))
+        _check("gdr_chunk_bwd_saved", rc)
+        return
+    ws = bwd_workspace(args, device)
     rc = lib.gdr_chunk_bwd(ctypes.byref(args), ctypes.byref(grads), ctypes.c_void_p(ws.data_ptr()),
-                           ctypes.c_int64(int(nbytes)), ctypes.c_void_p(stream))
-    if rc != 0:
-        raise RuntimeError(f"gdr_chunk_bwd failed ({rc}): {lib.gdr_last_error().decode()}")
+                           ctypes.c_int64(ws.numel()), ctypes.c_void_p(stream))
+    _check("gdr_chunk_bwd", rc)
 
 
 def _check(entry: str, rc: int) -> None:

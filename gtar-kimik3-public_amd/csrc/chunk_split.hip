@@ -40,6 +40,9 @@ using namespace chunk;
 
 namespace {
 
+// What the state scan writes (chunk_scan_kernel's kMode).
+constexpr int kScanOut = 0, kScanStates = 1, kScanBoth = 2;
+
 // LDS of the prep kernel (bytes); 3 workgroups fit a CU for K = 128.
 template <int K>
 struct PrepLds {
@@ -797,14 +800,16 @@ struct ScanShape {
   static constexpr int kOP = SL + 8;                             // row pitch (elements) of the output tile in LDS
 };
 
-// kStates (backward recompute): instead of the output, write the state entering every chunk to `states` [NC][K][V]
-// (bf16, rounded as the MFMA operand) and the bf16 u to `ubuf` [NC * 64][V], per (sequence, head).
-template <int VARIANT, int K, typename OutT, int SL, int NT, bool kStates = false, typename T = __bf16>
+// kMode: kScanOut writes the output (and the final state); kScanStates (the backward's recompute) instead writes the
+// state entering every chunk to `states` [NC][K][V] (bf16, rounded as the MFMA operand) and the bf16 u to `ubuf`
+// [NC * 64][V], per (sequence, head), skipping the readout; kScanBoth (the forward for training) writes all of it.
+template <int VARIANT, int K, typename OutT, int SL, int NT, int kMode = kScanOut, typename T = __bf16>
 __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_kernel(const gdr_args a, int n_slices,
                                                                                 int xcd_map, int nc,
                                                                                 int64_t rec_bytes,
                                                                                 __bf16* __restrict__ states,
                                                                                 __bf16* __restrict__ ubuf) {
+  constexpr bool kSave = kMode != kScanOut, kOut = kMode != kScanStates;
   constexpr bool kDelta = VARIANT != GDR_GLA;
   constexpr int KT = K / 16, KS = K / 32;
   using V8 = vec8<T>;
@@ -886,13 +891,13 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
     lds_barrier();
     for (int s = 0; s < nchunks; ++s) {
       if (s + 1 < nchunks) copy_record(s + 1, (s + 1) & 1);  // buffer (s + 1) & 1 held chunk s - 1: done
-      if constexpr (!kStates) {
+      if constexpr (kOut) {
         if (s > 0) store_tile(s - 1);
       }
       __builtin_amdgcn_s_waitcnt(0);
       lds_barrier();
     }
-    if constexpr (!kStates) {
+    if constexpr (kOut) {
       if (nchunks > 0) store_tile(nchunks - 1);
     }
     return;
@@ -913,7 +918,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
   lds_barrier();
 
   const int V = a.value_dim;
-  const size_t st_base = size_t(n * H + h) * nc * K * V;  // kStates buffers (non-varlen only)
+  const size_t st_base = size_t(n * H + h) * nc * K * V;  // kSave buffers (non-varlen only)
   const size_t ub_base = size_t(n * H + h) * nc * kChunk * V;
   auto store_state = [&](int c) {
 #pragma unroll
@@ -928,7 +933,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
   OutT* otile = reinterpret_cast<OutT*>(smem + 2 * SB);
   for (int s = 0; s < nchunks; ++s) {
     const unsigned char* bb = smem + (s & 1) * SB;
-    if constexpr (kStates) store_state(s);
+    if constexpr (kSave) store_state(s);
     const T* wl = reinterpret_cast<const T*>(bb + R::W);
     const T* ql = reinterpret_cast<const T*>(bb + R::QD);
     const T* scl = reinterpret_cast<const T*>(bb + R::SC);
@@ -956,7 +961,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
         const int r0 = R::rk(16 * i + l16, 32 * kk + 8 * g4);  // permuted order: one 16-byte read
-        if constexpr (!kStates) fq[buf][kk] = *reinterpret_cast<const V8*>(ql + r0);
+        if constexpr (kOut) fq[buf][kk] = *reinterpret_cast<const V8*>(ql + r0);
         if constexpr (kDelta) fw[buf][kk] = *reinterpret_cast<const V8*>(wl + r0);
       }
     };
@@ -987,7 +992,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
       if (i + 1 < 4) {
         read_block(i + 1, (i + 1) & 1);
       } else {
-        if constexpr (!kStates) {
+        if constexpr (kOut) {
 #pragma unroll
           for (int q = 0; q < 10; ++q) fsc[q] = *reinterpret_cast<const V4*>(scl + q * 256 + l16 * 16 + 4 * g4);
         }
@@ -1002,7 +1007,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
       for (int kk = 0; kk < KS; ++kk) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          if constexpr (!kStates) ao[t] = mfma32(sB[t][kk], fq[i & 1][kk], ao[t]);
+          if constexpr (kOut) ao[t] = mfma32(sB[t][kk], fq[i & 1][kk], ao[t]);
           if constexpr (kDelta) ax[t] = mfma32(fw[i & 1][kk], sB[t][kk], ax[t]);
         }
       }
@@ -1013,7 +1018,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
         for (int r = 0; r < 4; ++r) u[r] = kDelta ? f32(uu[t][i][r]) - ax[t][r] : f32(uu[t][i][r]);
         ub[t][i] = pack4<T>(u);
         acc_ot[t][i] = ao[t];
-        if constexpr (kStates) {
+        if constexpr (kSave) {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             ubuf[ub_base + size_t(s * kChunk + 16 * i + 4 * g4 + r) * V + c0 + 16 * t + l16] = ub[t][i][r];
@@ -1024,7 +1029,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
     // of u_j, u_{j+1} are the A layout of [u_j u_{j+1}]^T in the two-tile k order, and the score tiles read like
     // Sc_ij give B in the same order (a block past i contributes zeros).  Every MFMA accumulating onto the readout
     // has the readout's shape, so no accumulator passes between MFMAs of different shapes.
-    if constexpr (!kStates) {
+    if constexpr (kOut) {
       const V4 z4 = {};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -1059,7 +1064,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
     }
     update_half(KT - 1, 1);
     // output: lane holds O[token 16 i + l16][columns c0 + 16 t + 4 g4 .. + 3], into the chunk's LDS tile
-    if constexpr (!kStates) {
+    if constexpr (kOut) {
       OutT* tw = otile + (s & 1) * 64 * kOP;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -1120,12 +1125,12 @@ int scan_slice(int64_t bh, int value_dim) {
   return 16;
 }
 
-template <int VARIANT, int K, typename OutT, int SL, int NT, bool kStates, typename T>
+template <int VARIANT, int K, typename OutT, int SL, int NT, int kMode, typename T>
 hipError_t launch_scan_sl(const gdr_args& a, int nc, __bf16* states, __bf16* ubuf, hipStream_t stream) {
   using Sh = ScanShape<SL, NT>;
-  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::ut_slice(SL)) + (kStates ? 0 : 2 * 64 * Sh::kOP * int(sizeof(OutT)));
+  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::ut_slice(SL)) + (kMode == kScanStates ? 0 : 2 * 64 * Sh::kOP * int(sizeof(OutT)));
   static_assert(scan_lds <= 160 * 1024, "scan LDS");
-  constexpr auto kernel = &chunk_scan_kernel<VARIANT, K, OutT, SL, NT, kStates, T>;
+  constexpr auto kernel = &chunk_scan_kernel<VARIANT, K, OutT, SL, NT, kMode, T>;
   hipError_t e = configure_lds<kernel>(scan_lds);
   if (e != hipSuccess) return e;
   const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
@@ -1137,14 +1142,14 @@ hipError_t launch_scan_sl(const gdr_args& a, int nc, __bf16* states, __bf16* ubu
   return hipGetLastError();
 }
 
-template <int VARIANT, int K, typename OutT, bool kStates, typename T = __bf16>
+template <int VARIANT, int K, typename OutT, int kMode, typename T = __bf16>
 hipError_t launch_scan(const gdr_args& a, __bf16* states, __bf16* ubuf, hipStream_t stream) {
   const int nc = (a.seq_len + kChunk - 1) / kChunk;
   const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
   switch (scan_slice(int64_t(n_seq) * a.heads, a.value_dim)) {
-    case 64: return launch_scan_sl<VARIANT, K, OutT, 64, 1, kStates, T>(a, nc, states, ubuf, stream);
-    case 32: return launch_scan_sl<VARIANT, K, OutT, 32, 1, kStates, T>(a, nc, states, ubuf, stream);
-    default: return launch_scan_sl<VARIANT, K, OutT, 16, 1, kStates, T>(a, nc, states, ubuf, stream);
+    case 64: return launch_scan_sl<VARIANT, K, OutT, 64, 1, kMode, T>(a, nc, states, ubuf, stream);
+    case 32: return launch_scan_sl<VARIANT, K, OutT, 32, 1, kMode, T>(a, nc, states, ubuf, stream);
+    default: return launch_scan_sl<VARIANT, K, OutT, 16, 1, kMode, T>(a, nc, states, ubuf, stream);
   }
 }
 
@@ -1153,7 +1158,7 @@ hipError_t launch_split_typed(const gdr_args& a, const gdr_prologue& pro, hipStr
   if (a.q.dtype == GDR_F16) {  // f16 q, k, v: f16 MFMA operands and records (plain op only)
     hipError_t e = launch_prep<VARIANT, K, 0, _Float16>(a, pro, stream);
     if (e != hipSuccess) return e;
-    return launch_scan<VARIANT, K, OutT, false, _Float16>(a, nullptr, nullptr, stream);
+    return launch_scan<VARIANT, K, OutT, kScanOut, _Float16>(a, nullptr, nullptr, stream);
   }
   hipError_t e;
   const bool conv = pro.flags & GDR_PRO_CONV;
@@ -1168,7 +1173,7 @@ hipError_t launch_split_typed(const gdr_args& a, const gdr_prologue& pro, hipStr
     e = conv ? launch_prep<VARIANT, K, 5>(a, pro, stream) : launch_prep<VARIANT, K, 1>(a, pro, stream);
   }
   if (e != hipSuccess) return e;
-  return launch_scan<VARIANT, K, OutT, false>(a, nullptr, nullptr, stream);
+  return launch_scan<VARIANT, K, OutT, kScanOut>(a, nullptr, nullptr, stream);
 }
 
 template <int VARIANT, int K>
@@ -1193,8 +1198,28 @@ hipError_t launch_states_typed(const gdr_args& fwd, const BwdLayout& L, unsigned
   a.ht = nullptr;
   hipError_t e = launch_prep<VARIANT, K, 0>(a, gdr_prologue{}, stream);
   if (e != hipSuccess) return e;
-  return launch_scan<VARIANT, K, __bf16, true>(a, reinterpret_cast<__bf16*>(ws + L.states),
+  return launch_scan<VARIANT, K, __bf16, kScanStates>(a, reinterpret_cast<__bf16*>(ws + L.states),
                                               reinterpret_cast<__bf16*>(ws + L.ubuf), stream);
+}
+
+// Forward for training: the records into the backward workspace, then the scan writing the output and the final
+// state together with the states and u that the backward reads.
+template <int VARIANT, int K>
+hipError_t launch_train_typed(const gdr_args& fwd, const BwdLayout& L, unsigned char* ws, hipStream_t stream) {
+  gdr_args a = fwd;
+  a.workspace = ws + L.rec;
+  hipError_t e = launch_prep<VARIANT, K, 0>(a, gdr_prologue{}, stream);
+  if (e != hipSuccess) return e;
+  __bf16* states = reinterpret_cast<__bf16*>(ws + L.states);
+  __bf16* ubuf = reinterpret_cast<__bf16*>(ws + L.ubuf);
+  return a.out.dtype == GDR_F32 ? launch_scan<VARIANT, K, float, kScanBoth>(a, states, ubuf, stream)
+                                : launch_scan<VARIANT, K, __bf16, kScanBoth>(a, states, ubuf, stream);
+}
+
+template <int VARIANT>
+hipError_t launch_train_v(const gdr_args& a, const BwdLayout& L, unsigned char* ws, hipStream_t stream) {
+  return a.key_dim == 64 ? launch_train_typed<VARIANT, 64>(a, L, ws, stream)
+                         : launch_train_typed<VARIANT, 128>(a, L, ws, stream);
 }
 
 template <int VARIANT>
@@ -1216,6 +1241,15 @@ hipError_t launch_chunk_states(const gdr_args& a, const BwdLayout& L, unsigned c
     case GDR_GDN: return launch_states_v<GDR_GDN>(a, L, ws, stream);
     case GDR_GLA: return launch_states_v<GDR_GLA>(a, L, ws, stream);
     default: return launch_states_v<GDR_DELTANET>(a, L, ws, stream);
+  }
+}
+
+hipError_t launch_chunk_train(const gdr_args& a, const BwdLayout& L, unsigned char* ws, hipStream_t stream) {
+  switch (a.variant) {
+    case GDR_KDA: return launch_train_v<GDR_KDA>(a, L, ws, stream);
+    case GDR_GDN: return launch_train_v<GDR_GDN>(a, L, ws, stream);
+    case GDR_GLA: return launch_train_v<GDR_GLA>(a, L, ws, stream);
+    default: return launch_train_v<GDR_DELTANET>(a, L, ws, stream);
   }
 }
 

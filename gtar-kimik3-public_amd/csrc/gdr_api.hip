@@ -202,6 +202,46 @@ int chunk_fwd(const gdr_args* a, const gdr_prologue* pro, hipStream_t stream) {
   return GDR_OK;
 }
 
+// Arguments of the chunk backward (both entry points) and its workspace.
+int check_bwd(const gdr_args* a, const gdr_grads* g, void* workspace, int64_t workspace_bytes) {
+  int rc = check_common(a, true, false);
+  if (rc) return rc;
+  if (!g) return fail(GDR_ERR_INVALID, "grads is NULL");
+  if (a->cu_seqlens) return fail(GDR_ERR_UNSUPPORTED, "the chunk backward does not take packed varlen input");
+  if (a->q.dtype != GDR_BF16 || a->k.dtype != GDR_BF16 || a->v.dtype != GDR_BF16)
+    return fail(GDR_ERR_UNSUPPORTED, "the chunk backward reads bf16 q, k, v (got dtype codes %d, %d, %d)", a->q.dtype,
+                a->k.dtype, a->v.dtype);
+  const bool has_gate = a->variant != GDR_DELTANET, has_beta = a->variant != GDR_GLA;
+  if ((rc = check_view(g->d_out, "d_out", true, false))) return rc;
+  if (g->d_out.dtype != GDR_BF16) return fail(GDR_ERR_UNSUPPORTED, "d_out must be bf16 (the MFMA operand type)");
+  if ((rc = check_view(g->d_query, "d_query", true, false))) return rc;
+  if ((rc = check_view(g->d_key, "d_key", true, false))) return rc;
+  if ((rc = check_view(g->d_value, "d_value", true, false))) return rc;
+  const gdr_tensor* outs[] = {&g->d_query, &g->d_key, &g->d_value};
+  const char* onames[] = {"d_query", "d_key", "d_value"};
+  for (int i = 0; i < 3; ++i)
+    if (outs[i]->dtype == GDR_F16) return fail(GDR_ERR_UNSUPPORTED, "%s: bf16 or f32 only", onames[i]);
+  if ((rc = check_view(g->d_gate, "d_gate", has_gate, true))) return rc;
+  if ((rc = check_view(g->d_beta, "d_beta", has_beta, true))) return rc;
+  if (!has_gate && g->d_gate.ptr) return fail(GDR_ERR_INVALID, "DeltaNet has no gate gradient");
+  if (!has_beta && g->d_beta.ptr) return fail(GDR_ERR_INVALID, "GLA has no beta gradient");
+  if ((reinterpret_cast<uintptr_t>(g->d_final) | reinterpret_cast<uintptr_t>(g->d_initial)) % 16 != 0)
+    return fail(GDR_ERR_INVALID, "d_final / d_initial must be 16-byte aligned");
+  const gdr_tensor* rows[] = {&a->q, &a->k, &a->v, &a->gate, &g->d_out};
+  const char* names[] = {"query", "key", "value", "gate", "d_out"};
+  for (int i = 0; i < 5; ++i) {
+    if (!rows[i]->ptr || (i == 3 && a->variant == GDR_GDN)) continue;
+    if ((rc = check_rows16(*rows[i], names[i]))) return rc;
+  }
+  const gdr::BwdLayout L = gdr::chunk_bwd_layout(*a);
+  if (!workspace) return fail(GDR_ERR_INVALID, "the chunk backward needs a workspace");
+  if (workspace_bytes < L.total)
+    return fail(GDR_ERR_INVALID, "workspace of %lld bytes given, %lld required", (long long)workspace_bytes,
+                (long long)L.total);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(GDR_ERR_INVALID, "workspace must be 256-byte aligned");
+  return GDR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -444,44 +484,53 @@ int64_t gdr_chunk_bwd_workspace_bytes(const gdr_args* a) {
 
 int gdr_chunk_bwd(const gdr_args* a, const gdr_grads* g, void* workspace, int64_t workspace_bytes,
                   hipStream_t stream) {
-  int rc = check_common(a, true, false);
+  const int rc = check_bwd(a, g, workspace, workspace_bytes);
   if (rc) return rc;
-  if (!g) return fail(GDR_ERR_INVALID, "grads is NULL");
+  const gdr::BwdLayout L = gdr::chunk_bwd_layout(*a);
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  hipError_t e = gdr::launch_chunk_states(*a, L, ws, stream);
+  if (e == hipSuccess) e = gdr::launch_chunk_bwd(*a, *g, L, ws, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "chunk backward launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
+int gdr_chunk_fwd_train(const gdr_args* a, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  int rc = check_common(a, true, true);
+  if (rc) return rc;
   if (a->cu_seqlens) return fail(GDR_ERR_UNSUPPORTED, "the chunk backward does not take packed varlen input");
   if (a->q.dtype != GDR_BF16 || a->k.dtype != GDR_BF16 || a->v.dtype != GDR_BF16)
     return fail(GDR_ERR_UNSUPPORTED, "the chunk backward reads bf16 q, k, v (got dtype codes %d, %d, %d)", a->q.dtype,
                 a->k.dtype, a->v.dtype);
-  const bool has_gate = a->variant != GDR_DELTANET, has_beta = a->variant != GDR_GLA;
-  if ((rc = check_view(g->d_out, "d_out", true, false))) return rc;
-  if (g->d_out.dtype != GDR_BF16) return fail(GDR_ERR_UNSUPPORTED, "d_out must be bf16 (the MFMA operand type)");
-  if ((rc = check_view(g->d_query, "d_query", true, false))) return rc;
-  if ((rc = check_view(g->d_key, "d_key", true, false))) return rc;
-  if ((rc = check_view(g->d_value, "d_value", true, false))) return rc;
-  const gdr_tensor* outs[] = {&g->d_query, &g->d_key, &g->d_value};
-  const char* onames[] = {"d_query", "d_key", "d_value"};
-  for (int i = 0; i < 3; ++i)
-    if (outs[i]->dtype == GDR_F16) return fail(GDR_ERR_UNSUPPORTED, "%s: bf16 or f32 only", onames[i]);
-  if ((rc = check_view(g->d_gate, "d_gate", has_gate, true))) return rc;
-  if ((rc = check_view(g->d_beta, "d_beta", has_beta, true))) return rc;
-  if (!has_gate && g->d_gate.ptr) return fail(GDR_ERR_INVALID, "DeltaNet has no gate gradient");
-  if (!has_beta && g->d_beta.ptr) return fail(GDR_ERR_INVALID, "GLA has no beta gradient");
-  if ((reinterpret_cast<uintptr_t>(g->d_final) | reinterpret_cast<uintptr_t>(g->d_initial)) % 16 != 0)
-    return fail(GDR_ERR_INVALID, "d_final / d_initial must be 16-byte aligned");
-  const gdr_tensor* rows[] = {&a->q, &a->k, &a->v, &a->gate, &g->d_out};
-  const char* names[] = {"query", "key", "value", "gate", "d_out"};
+  if (a->out.dtype != GDR_BF16 && a->out.dtype != GDR_F32)
+    return fail(GDR_ERR_UNSUPPORTED, "out: bf16 or f32 only");
+  if (a->workspace)
+    return fail(GDR_ERR_INVALID, "gdr_chunk_fwd_train: args->workspace must be NULL (the records go into the "
+                "backward workspace)");
+  const gdr_tensor* rows[] = {&a->q, &a->k, &a->v, &a->out, &a->gate};
+  const char* names[] = {"query", "key", "value", "out", "gate"};
   for (int i = 0; i < 5; ++i) {
-    if (!rows[i]->ptr || (i == 3 && a->variant == GDR_GDN)) continue;
+    if (!rows[i]->ptr || (i == 4 && a->variant == GDR_GDN)) continue;
     if ((rc = check_rows16(*rows[i], names[i]))) return rc;
   }
   const gdr::BwdLayout L = gdr::chunk_bwd_layout(*a);
-  if (!workspace) return fail(GDR_ERR_INVALID, "the chunk backward needs a workspace");
+  if (!workspace) return fail(GDR_ERR_INVALID, "gdr_chunk_fwd_train needs the backward workspace");
   if (workspace_bytes < L.total)
     return fail(GDR_ERR_INVALID, "workspace of %lld bytes given, %lld required", (long long)workspace_bytes,
                 (long long)L.total);
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(GDR_ERR_INVALID, "workspace must be 256-byte aligned");
-  unsigned char* ws = static_cast<unsigned char*>(workspace);
-  hipError_t e = gdr::launch_chunk_states(*a, L, ws, stream);
-  if (e == hipSuccess) e = gdr::launch_chunk_bwd(*a, *g, L, ws, stream);
+  const hipError_t e = gdr::launch_chunk_train(*a, L, static_cast<unsigned char*>(workspace), stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "chunk forward (training) launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
+int gdr_chunk_bwd_saved(const gdr_args* a, const gdr_grads* g, void* workspace, int64_t workspace_bytes,
+                        hipStream_t stream) {
+  const int rc = check_bwd(a, g, workspace, workspace_bytes);
+  if (rc) return rc;
+  const gdr::BwdLayout L = gdr::chunk_bwd_layout(*a);
+  const hipError_t e = gdr::launch_chunk_bwd(*a, *g, L, static_cast<unsigned char*>(workspace), stream);
   if (e != hipSuccess) return fail(GDR_ERR_HIP, "chunk backward launch failed: %s", hipGetErrorString(e));
   g_last_error.clear();
   return GDR_OK;

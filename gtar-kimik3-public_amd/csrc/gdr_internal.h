@@ -63,7 +63,11 @@ BwdLayout chunk_bwd_layout(const gdr_args& a);
 // states and ubuf instead of the output).  `ws` is the backward workspace.
 hipError_t launch_chunk_states(const gdr_args& a, const BwdLayout& L, unsigned char* ws, hipStream_t stream);
 
-// The backward proper (after launch_chunk_states): reverse state scan, state-side products, chunk-local gradients.
+// Forward for training: the chunk forward's output and final state, leaving in `ws` the records, states and u that
+// launch_chunk_bwd reads (what launch_chunk_states would recompute).
+hipError_t launch_chunk_train(const gdr_args& a, const BwdLayout& L, unsigned char* ws, hipStream_t stream);
+
+// The backward proper (after launch_chunk_states or launch_chunk_train): reverse state scan, chunk-local gradients.
 hipError_t launch_chunk_bwd(const gdr_args& a, const gdr_grads& g, const BwdLayout& L, unsigned char* ws,
                             hipStream_t stream);
 

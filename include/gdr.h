@@ -178,10 +178,24 @@ typedef struct gdr_grads {
 int gdr_chunk_bwd(const gdr_args* args, const gdr_grads* grads, void* workspace, int64_t workspace_bytes,
                   hipStream_t stream);
 
-/* Bytes of device workspace gdr_chunk_bwd needs (no pointer dereferenced), or a negative gdr_status.  It holds
- * the forward record plus the per-chunk states and state gradients (fp32), u and du (bf16) and the fp32
- * state-side products, the buffers the reference allocates per call (:540-553, :575-606). */
+/* Bytes of device workspace gdr_chunk_bwd needs (no pointer dereferenced), or a negative gdr_status.  It holds,
+ * per chunk and head, the forward record, the state entering the chunk and the gradient of the state leaving it
+ * (bf16), u and du (bf16): the buffers the reference allocates per call (:540-553, :575-606). */
 int64_t gdr_chunk_bwd_workspace_bytes(const gdr_args* args);
+
+/* The chunk forward of a training step, paired with gdr_chunk_bwd_saved: writes out and ht as gdr_chunk_fwd does and
+ * leaves in `workspace` (gdr_chunk_bwd_workspace_bytes(args) bytes, 256-aligned, alive until the backward) the
+ * forward records, the per-chunk states and u, so that the backward need not recompute them.  The reference's
+ * ChunkKimiDeltaAttention.forward (src/ops/kimi_delta_attention.py:534-558) saves only its inputs and its
+ * backward recomputes the states (:566-571); the pair here trades that recompute (a prep launch and a state scan)
+ * for the workspace's memory, held from forward to backward.  args->workspace must be NULL.  Limits as
+ * gdr_chunk_bwd (bf16 q, k, v; no cu_seqlens); out is bf16 or f32.  Results equal gdr_chunk_fwd's bit for bit. */
+int gdr_chunk_fwd_train(const gdr_args* args, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* gdr_chunk_bwd without the forward recompute: `workspace` as gdr_chunk_fwd_train left it, for the same args
+ * (the same tensors, unchanged since).  Gradients equal gdr_chunk_bwd's bit for bit. */
+int gdr_chunk_bwd_saved(const gdr_args* args, const gdr_grads* grads, void* workspace, int64_t workspace_bytes,
+                        hipStream_t stream);
 
 /* Recurrent forward (decode).  Replaces the `_recurrent_forward` Triton launch of
  *   recurrent_kimi_delta_attention     src/ops/kimi_delta_attention.py:666-692 (kernel :38-68)

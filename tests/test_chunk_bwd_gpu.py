@@ -5,10 +5,14 @@ Mirrors the reference's gradient check (src tests/test_kimi_delta_attention.py:4
 plus a final-state term, gradients for q, k, v, gate, beta and the initial state) over its grid of shapes and gate
 strengths (:107-114), for all four variants, plus the layer's transposed layout, partial requires_grad, an absent
 initial state and a longer sequence; fp32 values (which run the fp32 recurrence) are refused with a clear error.
+The op's default training path (gdr_chunk_fwd_train keeping records, states and u; gdr_chunk_bwd_saved) is checked
+bit for bit against the recompute path (GDR_CHUNK_BWD_RECOMPUTE=1: plain forward, gdr_chunk_bwd).
 
 Tolerance: max|d - d_ref| <= 2e-2 * max|d_ref| for dq, dk, dv, dbeta and d(initial state); 3e-2 for the gate
 gradient, a reverse cumulative sum over each chunk of terms that each carry bf16 operand rounding.
 """
+
+import os
 
 import pytest
 import torch
@@ -146,3 +150,48 @@ def test_chunk_backward_refuses_fp32_values():
     v = inp.value.float().requires_grad_()
     with pytest.raises(NotImplementedError, match="fp32"):
         CHUNK_FNS["kda"](inp.query, inp.key, v, inp.gate, inp.beta)
+
+
+def _grads(variant, inp, recompute, retain=False):
+    gen = torch.Generator().manual_seed(11)
+    d_out = torch.randn(inp.value.shape, generator=gen).to(inp.value.dtype).cuda()
+    d_final = torch.randn(inp.initial_state.shape, generator=gen).cuda()
+    old = os.environ.get("GDR_CHUNK_BWD_RECOMPUTE")
+    os.environ["GDR_CHUNK_BWD_RECOMPUTE"] = "1" if recompute else "0"
+    try:
+        gl = _leaves(inp, "cuda")
+        out, fin = _call(variant, gl, _gpu)
+        need = [x for x in gl if x is not None]
+        grads = torch.autograd.grad([out, fin], need, [d_out, d_final], retain_graph=retain)
+        again = torch.autograd.grad([out, fin], need, [d_out, d_final]) if retain else None
+    finally:
+        if old is None:
+            del os.environ["GDR_CHUNK_BWD_RECOMPUTE"]
+        else:
+            os.environ["GDR_CHUNK_BWD_RECOMPUTE"] = old
+    torch.cuda.synchronize()
+    return out.detach(), fin.detach(), grads, again
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_saved_forward_state_matches_recompute(variant):
+    """gdr_chunk_fwd_train + gdr_chunk_bwd_saved against the plain forward + gdr_chunk_bwd: outputs, final state and
+    every gradient bit for bit (the same kernels compute them; only who writes the states differs)."""
+    inp = workloads.make_inputs(variant, 2, 300, 4, 128, 128, seed=12, gate_scale=4.0, state_std=0.5)
+    o1, f1, g1, _ = _grads(variant, inp, recompute=False)
+    o2, f2, g2, _ = _grads(variant, inp, recompute=True)
+    assert torch.equal(o1, o2) and torch.equal(f1, f2)
+    with torch.no_grad():
+        gl = _leaves(inp, "cuda", requires=set())
+        o3, f3 = _call(variant, gl, _gpu)
+    assert torch.equal(o1, o3) and torch.equal(f1, f3)  # the training forward's output is the plain forward's
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+def test_saved_forward_state_second_backward():
+    """retain_graph: the saved workspace serves the first backward; the second recomputes, with equal results."""
+    inp = workloads.make_inputs("kda", 1, 200, 2, 64, 128, seed=13, state_std=1.0)
+    _, _, g1, g2 = _grads("kda", inp, recompute=False, retain=True)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
