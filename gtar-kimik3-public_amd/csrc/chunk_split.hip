@@ -798,13 +798,15 @@ struct ScanShape {
   static constexpr int kLoaders = 4;                             // loader waves
   static constexpr int kThreads = 64 * (kCompute + kLoaders);
   static constexpr int kOP = SL + 8;                             // row pitch (elements) of the output tile in LDS
+  static constexpr int kStorers = 2;                             // kSave modes: waves storing the state / u tiles
+  static constexpr int threads(int mode) { return kThreads + (mode != 0 ? 64 * kStorers : 0); }
 };
 
 // kMode: kScanOut writes the output (and the final state); kScanStates (the backward's recompute) instead writes the
 // state entering every chunk to `states` [NC][K][V] (bf16, rounded as the MFMA operand) and the bf16 u to `ubuf`
 // [NC * 64][V], per (sequence, head), skipping the readout; kScanBoth (the forward for training) writes all of it.
 template <int VARIANT, int K, typename OutT, int SL, int NT, int kMode = kScanOut, typename T = __bf16>
-__global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_kernel(const gdr_args a, int n_slices,
+__global__ __launch_bounds__((ScanShape<SL, NT>::threads(kMode)), 1) void chunk_scan_kernel(const gdr_args a, int n_slices,
                                                                                 int xcd_map, int nc,
                                                                                 int64_t rec_bytes,
                                                                                 __bf16* __restrict__ states,
@@ -819,6 +821,9 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
   using R = Rec<K>;
 
   constexpr int SB = R::FIX + R::ut_slice(SL);     // LDS bytes per buffer
+  constexpr int kSP = SL + 8;                      // bf16 pitch of the kSave tiles
+  constexpr int kSaveOff = 2 * SB + (kOut ? 2 * 64 * kOP * int(sizeof(OutT)) : 0);
+  static_assert(!kSave || (__is_same(T, __bf16) && NT == 1), "kSave: bf16 operands, one tile per wave");
   constexpr int NF = R::FIX / 16, NU = R::ut_slice(SL) / 16;
   constexpr int NG = ((NF + NU + 63) / 64 + kScanLoaders - 1) / kScanLoaders;  // 64-piece groups per loader wave
   extern __shared__ __align__(16) unsigned char smem[];
@@ -848,7 +853,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
   // wave index made explicitly wave-uniform so that role and group branches are scalar branches
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
 
-  if (wave >= kScanCompute) {
+  if (wave >= kScanCompute && wave < kScanCompute + kScanLoaders) {
     // ---------------- loader waves ----------------
     // The record of chunk s + 1 is copied straight into LDS buffer (s + 1) & 1 while the compute waves work on
     // chunk s (global_load_lds_dwordx4: each lane's 16 bytes land at the wave-uniform LDS base + 16 * lane).
@@ -903,6 +908,38 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
     return;
   }
 
+  if (wave >= kScanCompute) {
+    // ---------------- storer waves (kSave) ----------------
+    // The compute waves leave the state entering each chunk ([K][kSP]) and u ([64][kSP]) as bf16 in
+    // double-buffered LDS tiles; these waves store the previous chunk's tiles during the next step as 16-byte row
+    // pieces.  They never wait for their stores (the loaders' wait for the record copy, which precedes each
+    // barrier, would otherwise include them).
+    if constexpr (kSave) {
+      const int sw = wave - kScanCompute - kScanLoaders;
+      const __bf16* stile = reinterpret_cast<const __bf16*>(smem + kSaveOff);
+      auto store_save = [&](int chunk) {
+        constexpr int kRowPieces = SL / 8, kStorers = ScanShape<SL, NT>::kStorers;
+        const __bf16* sl = stile + (chunk & 1) * (K + kChunk) * kSP;
+        const size_t s0 = (size_t(n * H + h) * nc + chunk) * K * a.value_dim;
+        const size_t u0 = (size_t(n * H + h) * nc + chunk) * kChunk * a.value_dim;
+#pragma unroll
+        for (int pc = sw * 64 + lane; pc < (K + kChunk) * kRowPieces; pc += 64 * kStorers) {
+          const int row = pc / kRowPieces, col = (pc % kRowPieces) * 8;
+          const uint4 v = *reinterpret_cast<const uint4*>(sl + row * kSP + col);
+          __bf16* dst = row < K ? states + s0 + size_t(row) * a.value_dim : ubuf + u0 + size_t(row - K) * a.value_dim;
+          *reinterpret_cast<uint4*>(dst + v0 + col) = v;
+        }
+      };
+      lds_barrier();
+      for (int s = 0; s < nchunks; ++s) {
+        if (s > 0) store_save(s - 1);
+        lds_barrier();
+      }
+      if (nchunks > 0) store_save(nchunks - 1);
+    }
+    return;
+  }
+
   // ---------------- compute waves: NT 16-column tiles each ----------------
   const int l16 = lane & 15, g4 = lane >> 4;
   const int c0 = v0 + 16 * NT * wave;  // first column of this wave
@@ -917,17 +954,13 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
         st[t][m][r] = a.h0 ? a.h0[sbase + size_t(16 * m + 4 * g4 + r) * a.value_dim + c0 + 16 * t + l16] : 0.f;
   lds_barrier();
 
-  const int V = a.value_dim;
-  const size_t st_base = size_t(n * H + h) * nc * K * V;  // kSave buffers (non-varlen only)
-  const size_t ub_base = size_t(n * H + h) * nc * kChunk * V;
-  auto store_state = [&](int c) {
+  __bf16* stile = reinterpret_cast<__bf16*>(smem + kSaveOff);
+  auto store_state = [&](int c) {  // the state entering chunk c (bf16, the MFMA operand's rounding) into its tile
+    __bf16* tl = stile + (c & 1) * (K + kChunk) * kSP + (c0 - v0) + l16;
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+    for (int m = 0; m < KT; ++m)
 #pragma unroll
-      for (int m = 0; m < KT; ++m)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          states[st_base + (size_t(c) * K + 16 * m + 4 * g4 + r) * V + c0 + 16 * t + l16] = bf(st[t][m][r]);
+      for (int r = 0; r < 4; ++r) tl[(16 * m + 4 * g4 + r) * kSP] = bf(st[0][m][r]);
   };
 
   OutT* otile = reinterpret_cast<OutT*>(smem + 2 * SB);
@@ -1019,9 +1052,9 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::kThreads), 1) void chunk_scan_k
         ub[t][i] = pack4<T>(u);
         acc_ot[t][i] = ao[t];
         if constexpr (kSave) {
+          __bf16* tl = stile + (s & 1) * (K + kChunk) * kSP + (K + 16 * i + 4 * g4) * kSP + (c0 - v0) + l16;
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            ubuf[ub_base + size_t(s * kChunk + 16 * i + 4 * g4 + r) * V + c0 + 16 * t + l16] = ub[t][i][r];
+          for (int r = 0; r < 4; ++r) tl[r * kSP] = ub[t][i][r];
         }
       }
     }
@@ -1128,7 +1161,9 @@ int scan_slice(int64_t bh, int value_dim) {
 template <int VARIANT, int K, typename OutT, int SL, int NT, int kMode, typename T>
 hipError_t launch_scan_sl(const gdr_args& a, int nc, __bf16* states, __bf16* ubuf, hipStream_t stream) {
   using Sh = ScanShape<SL, NT>;
-  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::ut_slice(SL)) + (kMode == kScanStates ? 0 : 2 * 64 * Sh::kOP * int(sizeof(OutT)));
+  constexpr int scan_lds = 2 * (Rec<K>::FIX + Rec<K>::ut_slice(SL)) +
+                           (kMode == kScanStates ? 0 : 2 * 64 * Sh::kOP * int(sizeof(OutT))) +
+                           (kMode == kScanOut ? 0 : 2 * (K + kChunk) * (SL + 8) * 2);
   static_assert(scan_lds <= 160 * 1024, "scan LDS");
   constexpr auto kernel = &chunk_scan_kernel<VARIANT, K, OutT, SL, NT, kMode, T>;
   hipError_t e = configure_lds<kernel>(scan_lds);
@@ -1137,7 +1172,7 @@ hipError_t launch_scan_sl(const gdr_args& a, int nc, __bf16* states, __bf16* ubu
   const int bh = n_seq * a.heads;
   const int n_slices = a.value_dim / SL;
   const int xcd_map = (bh % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL(kernel, dim3(bh * n_slices), dim3(Sh::kThreads), scan_lds, stream, a, n_slices, xcd_map, nc,
+  hipLaunchKernelGGL(kernel, dim3(bh * n_slices), dim3(Sh::threads(kMode)), scan_lds, stream, a, n_slices, xcd_map, nc,
                      Rec<K>::bytes(a.value_dim), states, ubuf);
   return hipGetLastError();
 }
@@ -1146,11 +1181,16 @@ template <int VARIANT, int K, typename OutT, int kMode, typename T = __bf16>
 hipError_t launch_scan(const gdr_args& a, __bf16* states, __bf16* ubuf, hipStream_t stream) {
   const int nc = (a.seq_len + kChunk - 1) / kChunk;
   const int n_seq = a.cu_seqlens ? a.n_seqs : a.batch;
-  switch (scan_slice(int64_t(n_seq) * a.heads, a.value_dim)) {
-    case 64: return launch_scan_sl<VARIANT, K, OutT, 64, 1, kMode, T>(a, nc, states, ubuf, stream);
-    case 32: return launch_scan_sl<VARIANT, K, OutT, 32, 1, kMode, T>(a, nc, states, ubuf, stream);
-    default: return launch_scan_sl<VARIANT, K, OutT, 16, 1, kMode, T>(a, nc, states, ubuf, stream);
+  // The saving modes' extra LDS tiles cap the slice width: 32 columns (16 beside an fp32 output tile).
+  constexpr int kMaxSL = kMode == kScanOut ? 64 : (kMode == kScanBoth && sizeof(OutT) == 4 ? 16 : 32);
+  const int sl = std::min(scan_slice(int64_t(n_seq) * a.heads, a.value_dim), kMaxSL);
+  if constexpr (kMaxSL >= 64) {
+    if (sl == 64) return launch_scan_sl<VARIANT, K, OutT, 64, 1, kMode, T>(a, nc, states, ubuf, stream);
   }
+  if constexpr (kMaxSL >= 32) {
+    if (sl == 32) return launch_scan_sl<VARIANT, K, OutT, 32, 1, kMode, T>(a, nc, states, ubuf, stream);
+  }
+  return launch_scan_sl<VARIANT, K, OutT, 16, 1, kMode, T>(a, nc, states, ubuf, stream);
 }
 
 template <int VARIANT, int K, typename OutT>
