@@ -3,17 +3,19 @@
 //
 //   O[t] = sum_{s <= t} softmax_s(scale q_t . k_s) v_s       per (sequence, query head); key/value head h / (H / Hkv)
 //
-// One 512-thread workgroup owns 128 query rows of one (sequence, query head); wave w owns rows 16 w .. 16 w + 15.
-// Key/value tiles of 64 rows stream through double-buffered LDS (K and V rows XOR-swizzled by 16-byte chunk), loaded
-// straight into LDS (no registers) while the current tile is used.  Per tile and wave, on
-// v_mfma_f32_16x16x32_{bf16,f16}:
+// One 256-thread workgroup owns 128 query rows of one (sequence, query head); wave w owns the two 16-row blocks
+// 32 w + 16 b .. + 15 (b = 0, 1), so each K and V fragment it reads from LDS feeds both blocks' MFMAs (half the LDS
+// traffic per FLOP of one block per wave).  Key/value tiles of 64 rows stream through double-buffered LDS (K and V
+// rows XOR-swizzled by 16-byte chunk), loaded straight into LDS (no registers) while the current tile is used; two
+// workgroups share a CU.  Per tile, wave and row block, on v_mfma_f32_16x16x32_{bf16,f16}:
 //   * S^T = K Q^T  -- K rows from LDS as A, the wave's Q rows (registers for the whole call) as B, so each lane holds
 //     16 scores of one query row (lane % 16) and the online-softmax statistics stay per lane;
 //   * O^T += V^T P^T -- V^T through the transposing LDS read (ds_read_b64_tr_b16) as A, the bf16/f16 probabilities
 //     straight from the score registers as B (the key order inside a 32-key step is the one the score tiles give;
 //     the V^T read follows it), so O^T lands in the same per-query-row lane layout.
-// Scores are scaled into log2 units and exponentiated with v_exp_f32; fully masked tiles are computed and masked
-// (no MFMA sits under a data-dependent branch).
+// Scores are exponentiated with v_exp_f32 in log2 units (the scale folded into one FMA); only tiles crossing the
+// diagonal or the sequence end are masked, and the accumulators are rescaled only when a running max moved (uniform
+// branches around VALU work; no MFMA sits under a data-dependent branch).
 #include "chunk_common.h"
 #include "gdr_internal.h"
 
@@ -27,7 +29,8 @@ using chunk::pack4;
 
 constexpr int kBM = 128;  // query rows per workgroup
 constexpr int kBN = 64;   // keys per LDS tile
-constexpr int kAttnThreads = 512;
+constexpr int kAttnThreads = 256;
+constexpr int kRB = 2;  // 16-row query blocks per wave
 constexpr float kNegInf = -__builtin_inff();
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -66,7 +69,7 @@ __device__ __forceinline__ V8 cat(V4 lo, V4 hi) {
 __device__ __forceinline__ int attn_slot_base(const int32_t* cu, int n) { return cu[n] / kBM + n; }
 
 template <int D, typename T>
-__global__ __launch_bounds__(kAttnThreads, 4) void attention_fwd_kernel(const gdr_attention_args a, int nqb) {
+__global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gdr_attention_args a, int nqb) {
   using M = Mma<T>;
   using V8 = typename M::v8;
   using V4 = typename M::v4;
@@ -111,13 +114,17 @@ __global__ __launch_bounds__(kAttnThreads, 4) void attention_fwd_kernel(const gd
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, g4 = lane >> 4;
   const int q0 = qb * kBM;
-  const int qpos = q0 + 16 * wave + l16;  // this lane's query row (position in the sequence)
-  const int qrow = min(qpos, len - 1);
-
-  // Q rows as the B operand of S^T = K Q^T: lane (l16, g4) holds q[qpos][32 ds + 8 g4 .. + 7].
-  V8 qf[DS];
+  int qpos[kRB];  // this lane's query row of each block (position in the sequence)
+  // Q rows as the B operand of S^T = K Q^T: lane (l16, g4) holds q[qpos[b]][32 ds + 8 g4 .. + 7].
+  V8 qf[kRB][DS];
 #pragma unroll
-  for (int ds = 0; ds < DS; ++ds) qf[ds] = *reinterpret_cast<const V8*>(qp + int64_t(qrow) * a.q.stride_t + 32 * ds + 8 * g4);
+  for (int b = 0; b < kRB; ++b) {
+    qpos[b] = q0 + 16 * (kRB * wave + b) + l16;
+    const int qrow = min(qpos[b], len - 1);
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds)
+      qf[b][ds] = *reinterpret_cast<const V8*>(qp + int64_t(qrow) * a.q.stride_t + 32 * ds + 8 * g4);
+  }
 
   // ---- key/value tiles: global -> LDS directly (global_load_lds_dwordx4: a lane's 16 bytes land at the wave-
   // uniform LDS base + 16 * lane).  Row r, chunk c of a tile is stored at chunk c ^ (r mod DC), so each lane loads
@@ -142,10 +149,15 @@ __global__ __launch_bounds__(kAttnThreads, 4) void attention_fwd_kernel(const gd
   };
 
   const float c = a.scale * kLog2e;  // scores in log2 units
-  float m = kNegInf, l = 0.f;      // running max (log2 units) and sum for this lane's query row
-  floatx4 o[DT];
+  float m[kRB], l[kRB];               // running max (log2 units) and sum of this lane's query rows
+  floatx4 o[kRB][DT];
 #pragma unroll
-  for (int t = 0; t < DT; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < kRB; ++b) {
+    m[b] = kNegInf;
+    l[b] = 0.f;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[b][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
 
   issue_tile(0, 0);
   __builtin_amdgcn_s_waitcnt(0);
@@ -155,53 +167,77 @@ __global__ __launch_bounds__(kAttnThreads, 4) void attention_fwd_kernel(const gd
     if (kb + 1 < nkb) issue_tile(kb + 1, buf ^ 1);  // every wave is done with that buffer (tile kb - 1)
     const T* kt = ks + buf * TILE;
 
-    // S^T tiles: lane holds S[qpos][kb * kBN + 16 t + 4 g4 + i]
-    floatx4 s[4];
+    // S^T tiles: lane holds S[qpos[b]][kb * kBN + 16 t + 4 g4 + i]; each K fragment serves both row blocks
+    floatx4 s[kRB][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int b = 0; b < kRB; ++b) s[b][t] = floatx4{0.f, 0.f, 0.f, 0.f};
       const int row = 16 * t + l16;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
         const V8 kf = *reinterpret_cast<const V8*>(kt + row * D + (((4 * ds + g4) ^ (row % DC)) << 3));
-        s[t] = M::run(kf, qf[ds], s[t]);
+#pragma unroll
+        for (int b = 0; b < kRB; ++b) s[b][t] = M::run(kf, qf[b][ds], s[b][t]);
       }
     }
-    float mx = kNegInf;
+    // Only a tile that crosses this wave's diagonal or the sequence end needs the causal mask (a uniform branch).
+    const bool full = (kb + 1) * kBN - 1 <= q0 + 32 * wave && (kb + 1) * kBN <= len;
+    if (!full) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+      for (int b = 0; b < kRB; ++b)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kb * kBN + 16 * t + 4 * g4 + i;
-        s[t][i] = key <= qpos && key < len ? s[t][i] * c : kNegInf;
-        mx = fmaxf(mx, s[t][i]);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m, mx);
-    const float base = m_new == kNegInf ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m - base);
-    float rs = 0.f;
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+          for (int i = 0; i < 4; ++i) {
+            const int key = kb * kBN + 16 * t + 4 * g4 + i;
+            if (!(key <= qpos[b] && key < len)) s[b][t][i] = kNegInf;
+          }
+    }
+    float alpha[kRB];
+    V8 pf[kRB][2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[t][i] = __builtin_amdgcn_exp2f(s[t][i] - base);
-        rs += s[t][i];
-      }
-    rs += __shfl_xor(rs, 16, kWave);
-    rs += __shfl_xor(rs, 32, kWave);
-    l = l * alpha + rs;
-    m = m_new;
-    V8 pf[2];
+    for (int b = 0; b < kRB; ++b) {
+      float mx = kNegInf;  // of the raw scores; the scale c > 0 is applied once, inside the exponent's FMA
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) pf[s2] = cat<V4, V8>(M::pack(s[2 * s2]), M::pack(s[2 * s2 + 1]));
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[b][t][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float m_new = fmaxf(m[b], mx * c);
+      const float base = m_new == kNegInf ? 0.f : m_new;
+      alpha[b] = __builtin_amdgcn_exp2f(m[b] - base);
+      float rs = 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s[b][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[b][t][i], c, -base));
+          rs += s[b][t][i];
+        }
+      rs += __shfl_xor(rs, 16, kWave);
+      rs += __shfl_xor(rs, 32, kWave);
+      l[b] = l[b] * alpha[b] + rs;
+      m[b] = m_new;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) pf[b][s2] = cat<V4, V8>(M::pack(s[b][2 * s2]), M::pack(s[b][2 * s2 + 1]));
+    }
 
-    // O^T += V^T P^T: V^T rows 32 s2 + 4 g4 + r (and + 16), column 16 t + l16, through the transposing read
+    // O^T += V^T P^T: V^T rows 32 s2 + 4 g4 + r (and + 16), column 16 t + l16, through the transposing read; each
+    // V^T fragment serves both row blocks
+    // the running max moved for some lane: rescale the accumulators (alpha is exactly 1 where it did not)
+#pragma unroll
+    for (int b = 0; b < kRB; ++b) {
+      if (__any(alpha[b] != 1.f)) {
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[b][t][i] *= alpha[b];
+      }
+    }
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[t][i] *= alpha;
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         const int col = 16 * t + 4 * (l16 & 3);
@@ -210,21 +246,26 @@ __global__ __launch_bounds__(kAttnThreads, 4) void attention_fwd_kernel(const gd
         const int off1 = buf * TILE + r1 * D + (((col >> 3) ^ (r1 % DC)) << 3) + (col & 7);
         const V4 lo = __builtin_bit_cast(V4, lds_read_tr(reinterpret_cast<const unsigned char*>(vs), off0 * 2));
         const V4 hi = __builtin_bit_cast(V4, lds_read_tr(reinterpret_cast<const unsigned char*>(vs), off1 * 2));
-        o[t] = M::run(cat<V4, V8>(lo, hi), pf[s2], o[t]);
+        const V8 vf = cat<V4, V8>(lo, hi);
+#pragma unroll
+        for (int b = 0; b < kRB; ++b) o[b][t] = M::run(vf, pf[b][s2], o[b][t]);
       }
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile kb + 1 have landed
     __syncthreads();                 // ... everyone's, and every wave is done with tile kb
   }
 
-  if (qpos < len) {
-    const float inv = 1.f / l;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      floatx4 y = o[t];
+  for (int b = 0; b < kRB; ++b) {
+    if (qpos[b] < len) {
+      const float inv = 1.f / l[b];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) y[i] *= inv;
-      *reinterpret_cast<V4*>(op + int64_t(qpos) * a.out.stride_t + 16 * t + 4 * g4) = M::pack(y);
+      for (int t = 0; t < DT; ++t) {
+        floatx4 y = o[b][t];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] *= inv;
+        *reinterpret_cast<V4*>(op + int64_t(qpos[b]) * a.out.stride_t + 16 * t + 4 * g4) = M::pack(y);
+      }
     }
   }
 }
