@@ -21,8 +21,9 @@ One JSON line on stdout:
   * stack: the packed-prefill configuration through the hybrid stack harness (3 KDA blocks and 1 attention block
     of the 0.6B model's shapes, random bf16 weights, 32 sequences with lengths ~U[256, 4096]): end-to-end tokens/s
     and the KDA op's share of the time.
-  * train: the prefill configuration under torch.autograd, forward then backward (gdr_chunk_bwd), with the
-    backward's algorithmic bytes and HBM fraction.
+  * train: the prefill configuration under torch.autograd, the training forward (gdr_chunk_fwd_train) then the
+    backward (gdr_chunk_bwd_saved), steps queued back to back, with the backward's algorithmic bytes and HBM
+    fraction.
   * variants: the variant sweep configuration (Gated DeltaNet, GLA, DeltaNet and KDA at B=2, T=8192, H=16,
     dk=dv=128, bf16 q/k/v, fp32 gate/beta/state, no initial state): per op tokens/s, the HBM roofline with traffic
     and the bf16 MFMA fraction.
@@ -456,8 +457,9 @@ def train_bytes(B, T, H, K, V, **_):
 
 
 def bench_train(gdr, workloads, torch, steps, warmup):
-    """The prefill configuration's KDA op under torch.autograd: forward with grad, then backward (gdr_chunk_bwd)
-    for q, k, v, gate, beta and the initial state, with a random dO and final-state gradient."""
+    """The prefill configuration's KDA op under torch.autograd: the training forward (gdr_chunk_fwd_train, which
+    keeps the records, states and u), then the backward (gdr_chunk_bwd_saved) for q, k, v, gate, beta and the
+    initial state, with a random dO and final-state gradient."""
     cfg = PREFILL
     inp = workloads.make_inputs("kda", cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"], seed=0, state_std=0.02,
                                 device="cuda")
@@ -484,19 +486,19 @@ def bench_train(gdr, workloads, torch, steps, warmup):
         step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    fwd_ms, tot_ms = 0.0, 0.0
-    for _ in range(steps):
+    # Steps are queued back to back, as a training loop runs them (the host stays ahead of the GPU), with one
+    # synchronisation after the last: the events then time the GPU's work, not the host's dispatch of each step.
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for e in ev:
         clear_grads()
-        ev[0].record(stream)
+        e[0].record(stream)
         out, final = forward()
-        ev[1].record(stream)
+        e[1].record(stream)
         torch.autograd.backward([out, final], [d_out, d_final])
-        ev[2].record(stream)
-        torch.cuda.synchronize()
-        fwd_ms += ev[0].elapsed_time(ev[1])
-        tot_ms += ev[0].elapsed_time(ev[2])
-    fwd_ms, tot_ms = fwd_ms / steps, tot_ms / steps
+        e[2].record(stream)
+    torch.cuda.synchronize()
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    tot_ms = sum(e[0].elapsed_time(e[2]) for e in ev) / steps
     bwd_ms = tot_ms - fwd_ms
     tokens = cfg["B"] * cfg["T"]
     nbytes = train_bytes(**cfg)
