@@ -584,6 +584,22 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
     unsigned char* X2B = smem + L::R1 + buf * L::PB;
     unsigned char* DOB = smem + L::R2 + buf * L::PB;
     unsigned char* UB = smem + L::R3 + buf * L::PB;
+    // this pass's global operands first, so their latency overlaps the staging below: du^T for X2, v for
+    // rowsum(X2 (x) V), and the S / dS' rows of channel d
+    bf16x8 adu[NRT][2], sfr[2], dsfr[2];
+    bf16x4 vv[NRT];
+#pragma unroll
+    for (int x = 0; x < NRT; ++x) {
+      const int v = v0 + 16 * (rb + x);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) adu[x][kb] = ld8(dutg + size_t(v + l16) * kChunk + 32 * kb + 8 * g4);
+      if constexpr (kDelta) vv[x] = ld4(vp + int64_t(t0 + min(16 * tb + l16, nvalid - 1)) * a.v.stride_t + v + 4 * g4);
+    }
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      sfr[kv] = ld8(Sg + v0 + 32 * kv + 8 * g4);
+      dsfr[kv] = ld8(dSg + v0 + 32 * kv + 8 * g4);
+    }
     // dO and u columns [v0, v0 + 64), rows past the sequence end as zeros (the buffers written here were last read
     // two passes ago, before the previous pass's barrier)
     for (int idx = tid; idx < 64 * 8; idx += 64 * NW) {
@@ -604,13 +620,13 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const int s0 = 32 * kb + 8 * g4;
-        bf16x8 adu = *reinterpret_cast<const bf16x8*>(dutg + size_t(v + l16) * kChunk + s0);
+        bf16x8 du8 = adu[x][kb];
         if (s0 + 8 > nvalid) {
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            if (s0 + e >= nvalid) adu[e] = bf(0.f);
+            if (s0 + e >= nvalid) du8[e] = bf(0.f);
         }
-        acc = mfma32(adu, aB[kb], acc);
+        acc = mfma32(du8, aB[kb], acc);
       }
       const int t = 16 * tb + l16;
       const float bt = kDelta ? BETA[t] : 1.f;
@@ -621,9 +637,8 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
         for (int r = 0; r < 4; ++r) store_grad(g.d_value, off + r, bt * acc[r]);
       }
       if constexpr (kDelta) {
-        const bf16x4 vv = ld4(vp + int64_t(t0 + min(t, nvalid - 1)) * a.v.stride_t + v + 4 * g4);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dbv += acc[r] * f32(vv[r]);
+        for (int r = 0; r < 4; ++r) dbv += acc[r] * f32(vv[x][r]);
         *reinterpret_cast<bf16x4*>(X2B + pb_off(t, vl + 4 * g4)) = pack4(acc);
       }
     }
@@ -631,16 +646,16 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
 #pragma unroll
     for (int kv = 0; kv < 2; ++kv) {
       const int lc = 32 * kv + 8 * g4;
-      const bf16x8 sfr = ld8(Sg + v0 + lc), dsfr = ld8(dSg + v0 + lc);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) bnd += f32(sfr[e]) * f32(dsfr[e]);
+      for (int e = 0; e < 8; ++e) bnd += f32(sfr[kv][e]) * f32(dsfr[kv][e]);
       const bf16x8 us = *reinterpret_cast<const bf16x8*>(UB + pb_off(16 * tb + l16, lc));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = 16 * i + l16;
-        qd[i] = mfma32(*reinterpret_cast<const bf16x8*>(DOB + pb_off(row, lc)), sfr, qd[i]);
-        kt[i] = mfma32(*reinterpret_cast<const bf16x8*>(UB + pb_off(row, lc)), dsfr, kt[i]);
-        if constexpr (kDelta) x1[i] = mfma32(*reinterpret_cast<const bf16x8*>(X2B + pb_off(row, lc)), sfr, x1[i]);
+        qd[i] = mfma32(*reinterpret_cast<const bf16x8*>(DOB + pb_off(row, lc)), sfr[kv], qd[i]);
+        kt[i] = mfma32(*reinterpret_cast<const bf16x8*>(UB + pb_off(row, lc)), dsfr[kv], kt[i]);
+        if constexpr (kDelta)
+          x1[i] = mfma32(*reinterpret_cast<const bf16x8*>(X2B + pb_off(row, lc)), sfr[kv], x1[i]);
       }
 #pragma unroll
       for (int ii = 0; ii < NRT; ++ii) {
