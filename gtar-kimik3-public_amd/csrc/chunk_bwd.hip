@@ -63,7 +63,8 @@ __global__ __launch_bounds__(kDScanThreads, 1) void chunk_dscan_kernel(const gdr
   constexpr int DO = R::FIX;                           // dO slice: bf16 [64][64], 16-byte chunks swizzled by row
   constexpr int SB = R::FIX + kChunk * kScanSlice * 2;  // LDS bytes per buffer
   constexpr int NF = R::FIX / 16, NDO = kChunk * kScanSlice * 2 / 16;
-  constexpr int NG = ((NF + NDO + 63) / 64 + 3) / 4;   // 64-piece groups per loader wave
+  constexpr int G0 = kDelta ? 0 : R::QD / 1024;        // GLA reads no W: its copies start at Q e^B
+  constexpr int NG = ((NF + NDO + 63) / 64 - G0 + 3) / 4;  // 64-piece groups per loader wave
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int xb = blockIdx.x;
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(kDScanThreads, 1) void chunk_dscan_kernel(const gdr
       unsigned char* dst = smem + buf * SB;
 #pragma unroll
       for (int k = 0; k < NG; ++k) {
-        const int grp = lw + 4 * k;
+        const int grp = G0 + lw + 4 * k;
         const int idx = 64 * grp + lane;
         if (idx < NF + NDO) {
           const void* from;

@@ -825,7 +825,9 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::threads(kMode)), 1) void chunk_
   constexpr int kSaveOff = 2 * SB + (kOut ? 2 * 64 * kOP * int(sizeof(OutT)) : 0);
   static_assert(!kSave || (__is_same(T, __bf16) && NT == 1), "kSave: bf16 operands, one tile per wave");
   constexpr int NF = R::FIX / 16, NU = R::ut_slice(SL) / 16;
-  constexpr int NG = ((NF + NU + 63) / 64 + kScanLoaders - 1) / kScanLoaders;  // 64-piece groups per loader wave
+  // GLA reads no W (u = U): its copies start at the record's Q e^B
+  constexpr int G0 = kDelta ? 0 : R::QD / 1024;                 // first 64-piece group copied
+  constexpr int NG = ((NF + NU + 63) / 64 - G0 + kScanLoaders - 1) / kScanLoaders;  // 64-piece groups per loader wave
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int xb = blockIdx.x;
@@ -866,7 +868,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::threads(kMode)), 1) void chunk_
       unsigned char* dst = smem + buf * SB;
 #pragma unroll
       for (int k = 0; k < NG; ++k) {
-        const int g = lw + kScanLoaders * k;  // group of 64 16-byte pieces
+        const int g = G0 + lw + kScanLoaders * k;  // group of 64 16-byte pieces
         const int idx = 64 * g + lane;
         if (idx < NF + NU) {
           const int off = idx < NF ? idx * 16 : ut_off + (idx - NF) * 16;
