@@ -40,6 +40,12 @@ using namespace chunk;
 
 namespace {
 
+// A compile-time int passed to a generic lambda.
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};
+
 // What the state scan writes (chunk_scan_kernel's kMode).
 constexpr int kScanOut = 0, kScanStates = 1, kScanBoth = 2;
 
@@ -207,10 +213,12 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
 // ======================================= prep: one workgroup per (chunk, head) =======================================
 // kPro: the fused layer prologue.  0: none (the plain op); 1: `pro.flags` selects the in-kernel q / k
 // normalisation and the beta sigmoid; 2: as 1, and the per-channel gate comes from the low-rank projection; plus 4:
-// the short convolutions of q, k, v run in the kernel too.
+// the short convolutions of q, k, v run in the kernel too.  Three workgroups fit a CU's LDS; the f16 build, whose
+// diagonal strip tile carries extra bf16 operands, is held to two so that it does not spill.
 template <int VARIANT, int K, int kPro = 0, typename T = __bf16>
-__global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr_args a, int nc, int64_t rec_bytes,
-                                                                       const gdr_prologue pro) {
+__global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_prep_kernel(const gdr_args a, int nc,
+                                                                                         int64_t rec_bytes,
+                                                                                         const gdr_prologue pro) {
   constexpr bool kLowRank = (kPro & 3) == 2;
   constexpr bool kConv = (kPro & 4) != 0;
   static_assert(!kLowRank || VARIANT == GDR_KDA || VARIANT == GDR_GLA, "low-rank gate: per-channel variants");
@@ -714,41 +722,62 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
   T* wrec = reinterpret_cast<T*>(rec + R::W);
   T* utrec = reinterpret_cast<T*>(rec + R::FIX);
   const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  auto solve_tile = [&](int rhs_off, int col0, bool is_w, int out_col0) {
-    V4 xs[4];
+  // One wave solves a group of column tiles together, block by block, so that their dependent MFMA chains
+  // interleave and the L and A_ii fragments are read once per block: NW tiles of W (column tiles first + 4 t of
+  // K e^B) and NU tiles of U (column tiles first + 4 u of the staged V pass, output columns out0 + 16 (first + 4 u)).
+  auto solve_group = [&](auto nw_c, auto nu_c, int first, int out0) {
+    constexpr int NW = decltype(nw_c)::value, NU = decltype(nu_c)::value, NT = NW + NU;
+    V4 rv[NT][4], xs[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int rhs_off = t < NW ? L::KD : L::VST, col0 = 16 * (first + 4 * (t < NW ? t : t - NW));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)  // rows 16 i + 4 g4 + r, column col0 + l16
+        rv[t][i] = lds_read_tr<T>(smem, rhs_off + ((16 * i + 4 * g4 + (l16 >> 2)) * KP + col0 + 4 * (l16 & 3)) * 2);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int off = rhs_off + ((16 * i + 4 * g4 + (l16 >> 2)) * KP + col0 + 4 * (l16 & 3)) * 2;
-      const V4 rv = lds_read_tr<T>(smem, off);  // rows 16 i + 4 g4 + r, column col0 + l16
-      floatx4 z;
+      floatx4 z[NT];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) z[r] = f32(rv[r]);
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[t][r] = f32(rv[t][i][r]);
       if constexpr (kDelta) {
+        const float4 b4 = *reinterpret_cast<const float4*>(sbeta + 16 * i + 4 * g4);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) z[r] *= sbeta[16 * i + 4 * g4 + r];
+        for (int t = 0; t < NT; ++t) z[t][0] *= b4.x, z[t][1] *= b4.y, z[t][2] *= b4.z, z[t][3] *= b4.w;
 #pragma unroll
         for (int j = 0; j < i; ++j) {
           const V4 nl = *reinterpret_cast<const V4*>(negl + strict_tile(i, j) * 256 + l16 * 16 + 4 * g4);
-          z = mfma16(nl, xs[j], z);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) z[t] = mfma16(nl, xs[t][j], z[t]);
         }
         const V4 ai = *reinterpret_cast<const V4*>(ainv + i * 256 + l16 * 16 + 4 * g4);
-        const V4 zb = pack4<T>(z);
-        xs[i] = pack4<T>(mfma16(ai, zb, zero4));
-        if (is_w) {
-          // X_i^T: row 16 i + l16, channels out_col0 + 4 g4 + r, stored in the permuted channel order
-          const V4 xt = pack4<T>(mfma16(zb, ai, zero4));
-          const int wpos = 32 * (out_col0 >> 5) + 8 * g4 + 4 * ((out_col0 >> 4) & 1);
-          *reinterpret_cast<V4*>(wrec + R::rk(16 * i + l16, wpos)) = xt;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const V4 zb = pack4<T>(z[t]);
+          xs[t][i] = pack4<T>(mfma16(ai, zb, zero4));
+          if (t < NW) {
+            // X_i^T: row 16 i + l16, channels col0 + 4 g4 + r, stored in the permuted channel order
+            const int col0 = 16 * (first + 4 * t);
+            const V4 xt = pack4<T>(mfma16(zb, ai, zero4));
+            const int wpos = 32 * (col0 >> 5) + 8 * g4 + 4 * ((col0 >> 4) & 1);
+            *reinterpret_cast<V4*>(wrec + R::rk(16 * i + l16, wpos)) = xt;
+          }
         }
       } else {
-        xs[i] = pack4<T>(z);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) xs[t][i] = pack4<T>(z[t]);
       }
-      if (!is_w) *reinterpret_cast<V4*>(utrec + R::rt(out_col0 + l16, 16 * i + 4 * g4)) = xs[i];
+#pragma unroll
+      for (int t = NW; t < NT; ++t) {
+        const int oc = out0 + 16 * (first + 4 * (t - NW));
+        *reinterpret_cast<V4*>(utrec + R::rt(oc + l16, 16 * i + 4 * g4)) = xs[t][i];
+      }
     }
   };
-  if constexpr (kDelta) {
-    for (int nt = wave; nt < K / 16; nt += 4) solve_tile(L::KD, 16 * nt, true, 16 * nt);
-  }
+  // Full passes (K value columns) give every wave K / 64 tiles of U; W has K / 64 tiles per wave.
+  constexpr int TW = kDelta ? K / 64 : 0, TU = K / 64;
   for (int pass = 0; pass < n_pass; ++pass) {
     if (pass > 0) {  // value dims beyond K: later passes staged synchronously
       load_v_pass(pass);
@@ -757,7 +786,15 @@ __global__ __launch_bounds__(256, kPro ? 3 : 1) void chunk_prep_kernel(const gdr
       lds_barrier();
     }
     const int tiles = pass_width(pass) / 16;
-    for (int nt = wave; nt < tiles; nt += 4) solve_tile(L::VST, 16 * nt, false, pass * K + 16 * nt);
+    if (tiles == K / 16) {
+      if (pass == 0) solve_group(IntC<TW>{}, IntC<TU>{}, wave, 0);
+      else solve_group(IntC<0>{}, IntC<TU>{}, wave, pass * K);
+    } else {
+      if constexpr (TW > 0) {
+        if (pass == 0) solve_group(IntC<TW>{}, IntC<0>{}, wave, 0);
+      }
+      for (int nt = wave; nt < tiles; nt += 4) solve_group(IntC<0>{}, IntC<1>{}, nt, pass * K);
+    }
   }
 
   // fused prologue: the last chunk of a sequence stores the last 3 inputs of each of its head's q, k, v channels,
