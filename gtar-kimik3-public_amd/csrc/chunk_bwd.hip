@@ -246,7 +246,9 @@ struct DLocalLds {
   static constexpr int DB = HOT + 4 * K;        // fp32 [NW][64] per-wave dbeta partials
   static constexpr int BP = K + 4;              // fp32 pitch of BB
   static constexpr int BB = DB + NW * 256;      // fp32 [64][BP] block-local log2-gate cumsum (row-owned scan)
-  static constexpr int BYTES = BB + 64 * BP * 4;
+  static constexpr int kPre = 2;                // value passes whose dO, u and du^T are fetched at the start
+  static constexpr int DOU = BB + 64 * BP * 4;  // [kPre][dO, u, du^T] swizzled pass buffers, filled by LDS DMA
+  static constexpr int BYTES = DOU + kPre * 3 * PB;
   static_assert(2 * 64 * DP * 2 <= RB, "dSc and dP fit R4");
   static_assert((2 * NW * 64 + NW) * 4 <= RB, "the GDN row sums fit R1");
 };
@@ -267,6 +269,26 @@ __device__ __forceinline__ floatx4 mfma_f32(float a, float b, floatx4 c) {
 __device__ __forceinline__ void store_grad(const gdr_tensor& t, int64_t off, float v) {
   if (t.dtype == GDR_F32) static_cast<float*>(const_cast<void*>(t.ptr))[off] = v;
   else static_cast<__bf16*>(const_cast<void*>(t.ptr))[off] = bf(v);
+}
+
+// Four consecutive elements of a gradient row (the last dimension is contiguous): one 16-byte (fp32) or 8-byte (bf16)
+// store where the address is aligned for it, else four element stores.
+__device__ __forceinline__ void store_grad4(const gdr_tensor& t, int64_t off, floatx4 v) {
+  if (t.dtype == GDR_F32) {
+    float* p = static_cast<float*>(const_cast<void*>(t.ptr)) + off;
+    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+      *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+      return;
+    }
+  } else {
+    __bf16* p = static_cast<__bf16*>(const_cast<void*>(t.ptr)) + off;
+    if ((reinterpret_cast<uintptr_t>(p) & 7) == 0) {
+      *reinterpret_cast<bf16x4*>(p) = pack4(v);
+      return;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) store_grad(t, off + r, v[r]);
 }
 
 // Byte offset of (row, col) in a swizzled bf16 [64][64] pass buffer: 16-byte chunk q of row r sits at chunk q ^ (r % 8).
@@ -333,84 +355,113 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
     return kGate == 2 ? gp[tt * a.gate.stride_t + ch] : gp[tt * a.gate.stride_t];
   };
   const floatx4 z4 = {0.f, 0.f, 0.f, 0.f};
+  const size_t cidx = size_t(bh) * nc + c;
+  const __bf16* ug = ubuf + cidx * kChunk * V;  // u [64][V]
+  const __bf16* dop = static_cast<const __bf16*>(g.d_out.ptr) + n * g.d_out.stride_b + h * g.d_out.stride_h;
 
-  // ---- 1. row-owned (waves 0..3, block p = w; lane: row 16 p + l16, channels 32 kk + 8 g4 + j): q, k rows into
-  // LDS; the log2-gate cumsum within the block (b); P's operands k e^{b} (A), k e^{b_15 - b} (B, via LDS) and the
-  // diagonal tile's k e^{+-(b - mid)}; block totals and hot-channel flags ----
-  bf16x8 lk[KS], ae[KS], af[KS];
-  bool any_hot_row = false;
-  if (w < 4) {
-    const int p = w, trow = 16 * p + l16;
+  // ---- 1. row-owned (block p = w mod 4; lane: row 16 p + l16, channels 32 kk + 8 g4 + j for this wave's KH channel
+  // groups kk0 .. kk0 + KH - 1; with eight waves, waves p and p + 4 take the two halves of the channels): q, k rows
+  // into LDS; the log2-gate cumsum within the block (b); P's operands k e^{b} (A), k e^{b_15 - b} (B, via LDS) and
+  // the diagonal tile's k e^{+-(b - mid)}; block totals and hot-channel flags ----
+  constexpr int KH = NW >= 8 ? KS / 2 : KS;  // 32-channel groups per wave in the row-owned phases
+  const int kk0 = NW >= 8 ? (w >> 2) * KH : 0;
+  bf16x8 lk[KH], ae[KH], af[KH];
+  {
+    const int p = w & 3, trow = 16 * p + l16;
     const bool valid = trow < nvalid;
     const int64_t tc = t0 + min(trow, nvalid - 1);
     const uint32_t keep = valid ? 0xffffffffu : 0u;
     __bf16* QL = reinterpret_cast<__bf16*>(smem + L::R1);
     __bf16* KL = reinterpret_cast<__bf16*>(smem + L::R2);
     __bf16* KAPL = reinterpret_cast<__bf16*>(smem + L::R3);
-    float bl[KS][8];
-    bf16x8 kr8[KS];
+    float bl[KH][8];
+    bf16x8 kr8[KH];
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      const int ch = 32 * kk + 8 * g4;
+    for (int x = 0; x < KH; ++x) {
+      const int ch = 32 * (kk0 + x) + 8 * g4;
       uint4 qr = *reinterpret_cast<const uint4*>(qp + tc * a.q.stride_t + ch);
       uint4 kr = *reinterpret_cast<const uint4*>(kp + tc * a.k.stride_t + ch);
       qr = make_uint4(qr.x & keep, qr.y & keep, qr.z & keep, qr.w & keep);
       kr = make_uint4(kr.x & keep, kr.y & keep, kr.z & keep, kr.w & keep);
       *reinterpret_cast<uint4*>(QL + trow * KP + ch) = qr;
       *reinterpret_cast<uint4*>(KL + trow * KP + ch) = kr;
-      kr8[kk] = __builtin_bit_cast(bf16x8, kr);
+      kr8[x] = __builtin_bit_cast(bf16x8, kr);
       if constexpr (kGate == 2) {
         const float4 g0 = *reinterpret_cast<const float4*>(gp + tc * a.gate.stride_t + ch);
         const float4 g1 = *reinterpret_cast<const float4*>(gp + tc * a.gate.stride_t + ch + 4);
-        bl[kk][0] = g0.x; bl[kk][1] = g0.y; bl[kk][2] = g0.z; bl[kk][3] = g0.w;
-        bl[kk][4] = g1.x; bl[kk][5] = g1.y; bl[kk][6] = g1.z; bl[kk][7] = g1.w;
+        bl[x][0] = g0.x; bl[x][1] = g0.y; bl[x][2] = g0.z; bl[x][3] = g0.w;
+        bl[x][4] = g1.x; bl[x][5] = g1.y; bl[x][6] = g1.z; bl[x][7] = g1.w;
       } else {
         const float gs = kGate == 1 ? gp[tc * a.gate.stride_t] : 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) bl[kk][j] = gs;
+        for (int j = 0; j < 8; ++j) bl[x][j] = gs;
       }
     }
-    if (kDelta && g4 == 0) BETA[trow] = valid ? betap[tc * a.beta.stride_t] : 0.f;
+    // dO and u columns of the first kPre value passes (token rows) and du^T rows of those columns, copied into
+    // their swizzled LDS buffers behind the row loads (global_load_lds_dwordx4: lane i lands at the wave's base +
+    // 16 i, i.e. row 8 (m mod 8) + i / 8 of the buffer, slot i % 8, which holds chunk (i % 8) ^ (row % 8) of the
+    // row).  dO rows past the sequence end read its last row; they and the u rows there are zeroed once the copies
+    // have landed (step 1b), and du^T's columns there are masked where they are used.
+    {
+      const int npre = min(V / 64, L::kPre);
+#pragma unroll
+      for (int k = 0; k < 3 * L::kPre * 8 / NW; ++k) {
+        const int m = w + NW * k, ps = m / 24, tn = (m >> 3) % 3, row = 8 * (m & 7) + (lane >> 3);
+        const int chunk8 = 8 * ((lane & 7) ^ (row & 7)), col = 64 * ps + chunk8;
+        const __bf16* src = tn == 0   ? dop + (t0 + min(row, nvalid - 1)) * int64_t(g.d_out.stride_t) + col
+                            : tn == 1 ? ug + size_t(row) * V + col
+                                      : dubt + (cidx * V + 64 * ps + row) * kChunk + chunk8;
+        if (ps < npre)
+          __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(smem + L::DOU + m * 1024),
+                                           16, 0, 0);
+      }
+    }
+    if (kDelta && kk0 == 0 && g4 == 0) BETA[trow] = valid ? betap[tc * a.beta.stride_t] : 0.f;
     const float kf = valid ? kLog2e : 0.f;
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk)
+    for (int x = 0; x < KH; ++x)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) bl[kk][j] = row_scan16(bl[kk][j] * kf);
-    bool hot_any = false;
+      for (int j = 0; j < 8; ++j) bl[x][j] = row_scan16(bl[x][j] * kf);
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      const int ch = 32 * kk + 8 * g4;
+    for (int x = 0; x < KH; ++x) {
+      const int ch = 32 * (kk0 + x) + 8 * g4;
       bf16x8 kap;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float b = bl[kk][j];
+        const float b = bl[x][j];
         const float top = __shfl(b, 16 * g4), bot = __shfl(b, 16 * g4 + 15);
         const bool hot = top - bot > kDiagSpan;
-        hot_any |= hot;
-        const float mid = 0.5f * (top + bot), kv = f32(kr8[kk][j]);
+        const float mid = 0.5f * (top + bot), kv = f32(kr8[x][j]);
         kap[j] = bf(kv * ex2(bot - b));
-        lk[kk][j] = bf(kv * ex2(b));
-        ae[kk][j] = bf(hot ? 0.f : kv * ex2(b - mid));
-        af[kk][j] = bf(hot ? 0.f : kv * ex2(mid - b));
+        lk[x][j] = bf(kv * ex2(b));
+        ae[x][j] = bf(hot ? 0.f : kv * ex2(b - mid));
+        af[x][j] = bf(hot ? 0.f : kv * ex2(mid - b));
         if (l16 == 0) HOTF[p * K + ch + j] = hot ? 1 : 0;
       }
       *reinterpret_cast<bf16x8*>(KAPL + trow * KP + ch) = kap;
       if constexpr (kGate != 0) {
-        *reinterpret_cast<float4*>(BB + trow * BP + ch) = make_float4(bl[kk][0], bl[kk][1], bl[kk][2], bl[kk][3]);
-        *reinterpret_cast<float4*>(BB + trow * BP + ch + 4) = make_float4(bl[kk][4], bl[kk][5], bl[kk][6], bl[kk][7]);
+        *reinterpret_cast<float4*>(BB + trow * BP + ch) = make_float4(bl[x][0], bl[x][1], bl[x][2], bl[x][3]);
+        *reinterpret_cast<float4*>(BB + trow * BP + ch + 4) = make_float4(bl[x][4], bl[x][5], bl[x][6], bl[x][7]);
       }
       if (l16 == 15) {
-        *reinterpret_cast<float4*>(TOT + p * K + ch) = make_float4(bl[kk][0], bl[kk][1], bl[kk][2], bl[kk][3]);
-        *reinterpret_cast<float4*>(TOT + p * K + ch + 4) = make_float4(bl[kk][4], bl[kk][5], bl[kk][6], bl[kk][7]);
+        *reinterpret_cast<float4*>(TOT + p * K + ch) = make_float4(bl[x][0], bl[x][1], bl[x][2], bl[x][3]);
+        *reinterpret_cast<float4*>(TOT + p * K + ch + 4) = make_float4(bl[x][4], bl[x][5], bl[x][6], bl[x][7]);
       }
     }
-    any_hot_row = __any(hot_any);
   }
 
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's pass-buffer copies have landed
   lds_barrier();
 
   // ---- 1b. column-owned (every wave, channel d): the in-chunk log2-gate cumsum B at rows 16 j + 4 g4 + r, the
   // block-local cumsum plus the totals of the blocks before ----
+  if (nvalid < kChunk) {  // the prefetched dO and u rows past the sequence end become zeros
+    for (int idx = tid; idx < L::kPre * 2 * 64 * 8; idx += 64 * NW) {
+      const int ps = idx >> 10, tn = (idx >> 9) & 1, row = (idx >> 3) & 63;
+      if (row >= nvalid)
+        *reinterpret_cast<uint4*>(smem + L::DOU + (3 * ps + tn) * L::PB + 16 * (idx & 511)) = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
   float bc[4][4];
   {
     float pre = 0.f;
@@ -422,7 +473,8 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
     }
   }
 
-  // ---- 2. q, k of channel d at rows 16 j + 4 g4 + r (the 16x16x16 B-operand layout); P's tiles of row block w ----
+  // ---- 2. q, k of channel d at rows 16 j + 4 g4 + r (the 16x16x16 B-operand layout); P's tiles of row block
+  // w mod 4 over this wave's channel groups ----
   bf16x4 qc[4], kc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -431,17 +483,17 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
     kc[j] = lds_read_tr(smem, L::R2 + 2 * (row * KP + col));
   }
   floatx4 pacc[3] = {z4, z4, z4}, pdiag = z4;
-  if (kDelta && w < 4) {
+  if constexpr (kDelta) {
     // P_pj = (k e^{b}) (k e^{b_15 - b})^T e^{a_{p-1} - a_j}: the last factor is 1 for j = p - 1, else the block
     // totals in between.  Tiles j >= p are computed and dropped: no MFMA under a branch.
     const __bf16* KAPL = reinterpret_cast<const __bf16*>(smem + L::R3);
-    const int p = w;
+    const int p = w & 3;
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       floatx4 acc = z4;
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        const int ch = 32 * kk + 8 * g4;
+      for (int x = 0; x < KH; ++x) {
+        const int ch = 32 * (kk0 + x) + 8 * g4;
         bf16x8 bk = *reinterpret_cast<const bf16x8*>(KAPL + (16 * j + l16) * KP + ch);
         if (j < p - 1) {
           float4 f0 = make_float4(0.f, 0.f, 0.f, 0.f), f1 = f0;
@@ -455,15 +507,30 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
 #pragma unroll
           for (int e = 0; e < 8; ++e) bk[e] = bf(f32(bk[e]) * ex2(fs[e]));
         }
-        acc = mfma32(lk[kk], bk, acc);
+        acc = mfma32(lk[x], bk, acc);
       }
       pacc[j] = acc;
     }
     // diagonal tile: (k e^{b - mid}) (k e^{mid - b})^T with mid the middle of the block's gate range
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) pdiag = mfma32(ae[kk], af[kk], pdiag);
+    for (int x = 0; x < KH; ++x) pdiag = mfma32(ae[x], af[x], pdiag);
+    if (NW >= 8 && w >= 4) {  // the second channel half's partial tiles, to R4 (unused until step 5)
+      floatx4* part = reinterpret_cast<floatx4*>(smem + L::R4) + p * 4 * 64 + lane;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) part[64 * j] = pacc[j];
+      part[64 * 3] = pdiag;
+    }
   }
   lds_barrier();  // the q and k rows are read: R1 takes P, R2 takes A
+
+  // v rows for rowsum(X2 (x) V), loaded one value pass ahead of their use (the first pass's before the inverse)
+  auto load_vv = [&](int v0, bf16x4 (&dst)[NRT]) {
+#pragma unroll
+    for (int x = 0; x < NRT; ++x)
+      dst[x] = ld4(vp + int64_t(t0 + min(16 * tb + l16, nvalid - 1)) * a.v.stride_t + v0 + 16 * (rb + x) + 4 * g4);
+  };
+  bf16x4 vnext[NRT];
+  if constexpr (kDelta) load_vv(0, vnext);
 
   bf16x8 aB[2];        // A[32 kb + 8 g4 + e][16 tb + l16]: B operand of X2^T = du^T A
   float pv[NRT][4];    // P at this wave's dL positions (16 (rb + ii) + 4 g4 + r, 16 tb + l16)
@@ -473,6 +540,18 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
     float* YS = reinterpret_cast<float*>(smem + L::R3);
     if (w < 4) {
       const int p = w;
+      if constexpr (NW >= 8) {  // plus the other channel half's partial tiles
+        const floatx4* part = reinterpret_cast<const floatx4*>(smem + L::R4) + p * 4 * 64 + lane;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const floatx4 o = part[64 * j];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pacc[j][r] += o[r];
+        }
+        const floatx4 o = part[64 * 3];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pdiag[r] += o[r];
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -481,7 +560,9 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
           const float off = j < 3 ? pacc[j < 3 ? j : 0][r] : 0.f;
           PL[(16 * p + t) * MP + 16 * j + l16] = j < p ? off : ((j == p && l16 < t) ? pdiag[r] : 0.f);
         }
-      if (any_hot_row) {
+      bool hot = false;  // any hot channel in this block
+      for (int ch = lane; ch < K; ch += 64) hot |= HOTF[p * K + ch] != 0;
+      if (__any(hot)) {
         // exact terms of the hot channels of the diagonal tile, pair (t, s < t) of the block, from the gates
         const __bf16* KL = reinterpret_cast<const __bf16*>(smem + L::R2);
         for (int q = lane; q < 120; q += 64) {
@@ -526,7 +607,10 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
       }
     }
     lds_barrier();
-    // Y = diag(beta) P[block i, :16 i] A[:16 i, block p] (wave-private scratch), A_ip = -A_ii Y (zero for p >= i)
+    // Y = diag(beta) P[block i, :16 i] A[:16 i, block p] (wave-private scratch), A_ip = -A_ii Y (zero for p >= i).
+    // Wave p reads only column block p of A (its own writes, and the zeros and diagonal blocks in place before the
+    // barrier above), A_ii and its own scratch, so the block rows need no barrier between them: a wave's LDS
+    // accesses complete in order.
 #pragma unroll
     for (int i = 1; i < 4; ++i) {
       if (w < 4) {
@@ -547,8 +631,8 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
           for (int r = 0; r < 4; ++r) AL[(16 * i + 4 * g4 + r) * MP + 16 * p + l16] = -zz[r];
         }
       }
-      lds_barrier();
     }
+    lds_barrier();
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -568,12 +652,9 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
 
   // ---- 4. passes over 64 value columns: X2 (dv, dbeta), then X1, dQd, dKt (channel tile w, all rows) and dSc,
   // dL (columns of block tb, this wave's row tiles), and bnd = rowsum(S (x) dS') of channel d ----
-  const size_t cidx = size_t(bh) * nc + c;
   const __bf16* Sg = states + (cidx * K + d) * V;     // row d of S
   const __bf16* dSg = dstates + (cidx * K + d) * V;   // row d of dS'
-  const __bf16* ug = ubuf + cidx * kChunk * V;        // u [64][V]
   const __bf16* dutg = dubt + cidx * V * kChunk;      // du^T [V][64]
-  const __bf16* dop = static_cast<const __bf16*>(g.d_out.ptr) + n * g.d_out.stride_b + h * g.d_out.stride_h;
   floatx4 x1[4], qd[4], kt[4], sc[NRT], dl[NRT];
 #pragma unroll
   for (int i = 0; i < 4; ++i) x1[i] = qd[i] = kt[i] = z4;
@@ -581,29 +662,37 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
   for (int ii = 0; ii < NRT; ++ii) sc[ii] = dl[ii] = z4;
   float bnd = 0.f, dbv = 0.f;
   for (int v0 = 0; v0 < V; v0 += 64) {
-    const int buf = (v0 >> 6) & 1;
+    const int buf = (v0 >> 6) & 1, ps = v0 >> 6;
+    const bool pre = ps < L::kPre;  // dO and u already in their LDS buffers
     unsigned char* X2B = smem + L::R1 + buf * L::PB;
-    unsigned char* DOB = smem + L::R2 + buf * L::PB;
-    unsigned char* UB = smem + L::R3 + buf * L::PB;
+    unsigned char* DOB = pre ? smem + L::DOU + 3 * ps * L::PB : smem + L::R2 + buf * L::PB;
+    unsigned char* UB = pre ? smem + L::DOU + (3 * ps + 1) * L::PB : smem + L::R3 + buf * L::PB;
+    const unsigned char* DUB = smem + L::DOU + (3 * ps + 2) * L::PB;  // du^T rows of the pass (pre only)
     // this pass's global operands first, so their latency overlaps the staging below: du^T for X2, v for
     // rowsum(X2 (x) V), and the S / dS' rows of channel d
     bf16x8 adu[NRT][2], sfr[2], dsfr[2];
     bf16x4 vv[NRT];
+    if constexpr (kDelta) {
+#pragma unroll
+      for (int x = 0; x < NRT; ++x) vv[x] = vnext[x];
+      if (v0 + 64 < V) load_vv(v0 + 64, vnext);
+    }
 #pragma unroll
     for (int x = 0; x < NRT; ++x) {
       const int v = v0 + 16 * (rb + x);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) adu[x][kb] = ld8(dutg + size_t(v + l16) * kChunk + 32 * kb + 8 * g4);
-      if constexpr (kDelta) vv[x] = ld4(vp + int64_t(t0 + min(16 * tb + l16, nvalid - 1)) * a.v.stride_t + v + 4 * g4);
+      for (int kb = 0; kb < 2; ++kb)
+        adu[x][kb] = pre ? *reinterpret_cast<const bf16x8*>(DUB + pb_off(16 * (rb + x) + l16, 32 * kb + 8 * g4))
+                         : ld8(dutg + size_t(v + l16) * kChunk + 32 * kb + 8 * g4);
     }
 #pragma unroll
     for (int kv = 0; kv < 2; ++kv) {
       sfr[kv] = ld8(Sg + v0 + 32 * kv + 8 * g4);
       dsfr[kv] = ld8(dSg + v0 + 32 * kv + 8 * g4);
     }
-    // dO and u columns [v0, v0 + 64), rows past the sequence end as zeros (the buffers written here were last read
-    // two passes ago, before the previous pass's barrier)
-    for (int idx = tid; idx < 64 * 8; idx += 64 * NW) {
+    // later passes: dO and u columns [v0, v0 + 64), rows past the sequence end as zeros (the buffers written here
+    // were last read two passes ago, before the previous pass's barrier)
+    for (int idx = pre ? 64 * 8 : tid; idx < 64 * 8; idx += 64 * NW) {
       const int row = idx >> 3, q = idx & 7;
       uint4 dv = make_uint4(0u, 0u, 0u, 0u), uv = make_uint4(0u, 0u, 0u, 0u);
       if (row < nvalid) {
@@ -634,8 +723,7 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
       if (t < nvalid) {
         const int64_t off =
             n * g.d_value.stride_b + h * g.d_value.stride_h + int64_t(t0 + t) * g.d_value.stride_t + v + 4 * g4;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) store_grad(g.d_value, off + r, bt * acc[r]);
+        store_grad4(g.d_value, off, floatx4{bt * acc[0], bt * acc[1], bt * acc[2], bt * acc[3]});
       }
       if constexpr (kDelta) {
 #pragma unroll
