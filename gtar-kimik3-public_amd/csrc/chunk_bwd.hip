@@ -304,17 +304,12 @@ __device__ __forceinline__ float pick4(bf16x4 x, int r) {
 }
 
 // Sums of the 16-lane rows (width 16) and of the four 16-lane groups (over lanes l, l + 16, l + 32, l + 48).
-__device__ __forceinline__ float sum16(float v) {
-  v += __shfl_xor(v, 1, 16);
-  v += __shfl_xor(v, 2, 16);
-  v += __shfl_xor(v, 4, 16);
-  v += __shfl_xor(v, 8, 16);
-  return v;
-}
-__device__ __forceinline__ float sum_groups(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+__device__ __forceinline__ float sum16(float v) { return row_sum16(v); }  // its lanes' associations differ
+__device__ __forceinline__ float sum_groups(float v) {                    // the same sum in every lane
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 template <int VARIANT, int K>
@@ -429,7 +424,7 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float b = bl[x][j];
-        const float top = __shfl(b, 16 * g4), bot = __shfl(b, 16 * g4 + 15);
+        const float top = row_lane<0>(b), bot = row_lane<15>(b);
         const bool hot = top - bot > kDiagSpan;
         const float mid = 0.5f * (top + bot), kv = f32(kr8[x][j]);
         kap[j] = bf(kv * ex2(bot - b));
@@ -787,8 +782,8 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
   bool hot[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    anc[j] = __shfl(bc[j][3], 48 + l16);  // a_j = B at row 16 j + 15
-    const float top = __shfl(bc[j][0], l16);
+    anc[j] = from_row<3>(bc[j][3]);  // a_j = B at row 16 j + 15
+    const float top = from_row<0>(bc[j][0]);
     mid[j] = 0.5f * (top + anc[j]);
     hot[j] = top - anc[j] > kDiagSpan;
   }
@@ -934,15 +929,12 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
         kex[i][r] = s;
         s += ktv[i][r];
       }
-      float incl = s;
-      float y = __shfl(incl, (lane + 48) & 63);
-      if (g4 >= 1) incl += y;
-      y = __shfl(incl, (lane + 32) & 63);
-      if (g4 >= 2) incl += y;
+      float total;
+      const float incl = rows_scan(s, false, total);  // over the groups g4' <= g4
       const float before = carry + (incl - s);
 #pragma unroll
       for (int r = 0; r < 4; ++r) kex[i][r] += before;
-      carry += __shfl(incl, 48 + l16);
+      carry += total;
     }
     carry = ex2(bend) * bnd;
 #pragma unroll
@@ -953,18 +945,15 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
         s += gtv[i][r];
         suf[r] = s;
       }
-      float incl = s;  // over the groups g4' >= g4
-      float y = __shfl(incl, (lane + 16) & 63);
-      if (g4 <= 2) incl += y;
-      y = __shfl(incl, (lane + 32) & 63);
-      if (g4 <= 1) incl += y;
+      float total;
+      const float incl = rows_scan(s, true, total);  // over the groups g4' >= g4
       const float after = carry + (incl - s);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = 16 * i + 4 * g4 + r;
         if (t < nvalid) dgp[int64_t(t0 + t) * g.d_gate.stride_t + d] = after + suf[r] + kex[i][r];
       }
-      carry += __shfl(incl, l16);
+      carry += total;
     }
   } else if constexpr (kGate == 1) {
     float* GPS = reinterpret_cast<float*>(smem + L::R1);  // [NW][64] row sums of GT, [NW][64] of the Kt role, [NW] bnd

@@ -122,6 +122,50 @@ __device__ __forceinline__ float row_scan16(float x) {
   return x;
 }
 
+// Cross-lane moves on the VALU (DPP and the gfx950 permlane swaps) instead of ds_bpermute round trips through LDS.
+// dpp_row<CTRL>: one DPP move within each 16-lane row (CTRL is the dpp_ctrl code, every lane of the row valid).
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+// Lane N of each 16-lane row, in every lane of that row (row_newbcast).
+template <int N>
+__device__ __forceinline__ float row_lane(float x) {
+  return dpp_row<0x150 + N>(x);
+}
+// Sum over the 16 lanes of each row (quad_perm [1,0,3,2] and [2,3,0,1], then the row rotated by 4 and by 8).  Every
+// lane of the row ends with the sum, but the association differs between its quads, so callers use one lane's.
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp_row<0xB1>(x);
+  x += dpp_row<0x4E>(x);
+  x += dpp_row<0x124>(x);
+  x += dpp_row<0x128>(x);
+  return x;
+}
+// Row R (lanes 16 R .. 16 R + 15) in every row, lane l reading lane 16 R + l % 16: v_permlane32_swap of two copies
+// gives the lower half's rows (first result) or the upper half's (second) in both halves, and v_permlane16_swap of
+// two copies of that gives its even row (first) or odd row (second) in every row.
+template <int R>
+__device__ __forceinline__ float from_row(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const unsigned h = R < 2 ? a[0] : a[1];
+  const auto b = __builtin_amdgcn_permlane16_swap(h, h, false, false);
+  return __uint_as_float((R & 1) ? b[1] : b[0]);
+}
+// Per lane l16 of the four 16-lane rows g = lane / 16: the inclusive prefix (rows g' <= g) or suffix (rows g' >= g) of
+// x over the rows, and the total of the four, in every lane: the row pairs (0, 1) and (2, 3) are combined with a
+// permlane16 swap, then the two pair sums with a permlane32 swap.
+__device__ __forceinline__ float rows_scan(float x, bool suffix, float& total) {
+  const int g = (threadIdx.x & 63) >> 4;
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float pair = __uint_as_float(p[0]) + __uint_as_float(p[1]);  // rows 0, 1: x0 + x1; rows 2, 3: x2 + x3
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(pair), __float_as_uint(pair), false, false);
+  const float lo = __uint_as_float(q[0]), hi = __uint_as_float(q[1]);  // x0 + x1 and x2 + x3, in every lane
+  total = lo + hi;
+  if (suffix) return ((g & 1) ? x : pair) + (g < 2 ? hi : 0.f);
+  return ((g & 1) ? pair : x) + (g >= 2 ? lo : 0.f);
+}
+
 // One channel of one row of the op's inputs, for the hot-channel fix-up: q, k (element type T) and the gate (per channel for
 // KDA / GLA, per token for GDN).
 template <typename T>
