@@ -203,8 +203,8 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[b][t][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      mx = xor_max(mx, 16);
+      mx = xor_max(mx, 32);
       const float m_new = fmaxf(m[b], mx * c);
       const float base = m_new == kNegInf ? 0.f : m_new;
       alpha[b] = __builtin_amdgcn_exp2f(m[b] - base);
@@ -216,8 +216,8 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
           s[b][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[b][t][i], c, -base));
           rs += s[b][t][i];
         }
-      rs += __shfl_xor(rs, 16, kWave);
-      rs += __shfl_xor(rs, 32, kWave);
+      rs = xor_sum(rs, 16);
+      rs = xor_sum(rs, 32);
       l[b] = l[b] * alpha[b] + rs;
       m[b] = m_new;
 #pragma unroll

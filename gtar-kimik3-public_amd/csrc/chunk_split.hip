@@ -441,10 +441,10 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
 #pragma unroll
       for (int j = 0; j < 8; ++j) sq += qf[j] * qf[j], sk += kf[j] * kf[j];
     }
-    sq += __shfl_xor(sq, 16, kWave);
-    sk += __shfl_xor(sk, 16, kWave);
-    sq += __shfl_xor(sq, 32, kWave);
-    sk += __shfl_xor(sk, 32, kWave);
+    sq = xor_sum(sq, 16);
+    sk = xor_sum(sk, 16);
+    sq = xor_sum(sq, 32);
+    sk = xor_sum(sk, 32);
     const float iq = 1.f / fmaxf(sqrtf(sq), 1e-12f), ik = 1.f / fmaxf(sqrtf(sk), 1e-12f);
     if (g4 == 0) snorm[16 * p + l16] = iq, snorm[64 + 16 * p + l16] = ik;  // for the hot-block fix-up
 #pragma unroll

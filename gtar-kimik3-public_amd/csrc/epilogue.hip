@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void norm_gate_kernel(const gdr_norm_gate_args
 #pragma unroll
     for (int e = 0; e < EPL; ++e) ss += to_f(xr[it][e]) * to_f(xr[it][e]);
 #pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 16);
+    for (int m = 8; m >= 1; m >>= 1) ss = xor_sum(ss, m);  // within the 16-lane row
     const float r = rsqrtf(ss / float(16 * EPL) + a.eps);
     Lane<OT, EPL> o;
 #pragma unroll

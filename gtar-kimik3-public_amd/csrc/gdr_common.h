@@ -44,4 +44,37 @@ __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp
 
 __device__ __forceinline__ float shfl_xor(float x, int mask) { return __shfl_xor(x, mask, kWave); }
 
+// x + x[lane ^ m] in every lane (m a power of two below 64, constant after unrolling), formed on the VALU where one
+// lane move gives exactly that partner: quad_perm for 1 and 2, the 16-lane row rotated by 8 for 8, and the gfx950
+// permlane swaps of two copies of x for 16 and 32 (whose two results hold the partner rows' values, so every lane
+// adds the same pair).  m = 4 goes through ds_bpermute.  Bit-identical to x + shfl_xor(x, m).
+__device__ __forceinline__ float xor_sum(float x, int m) {
+  const int xi = __float_as_int(x);
+  if (m == 1) return x + __int_as_float(__builtin_amdgcn_update_dpp(0, xi, 0xB1, 0xf, 0xf, false));   // [1,0,3,2]
+  if (m == 2) return x + __int_as_float(__builtin_amdgcn_update_dpp(0, xi, 0x4E, 0xf, 0xf, false));   // [2,3,0,1]
+  if (m == 8) return x + __int_as_float(__builtin_amdgcn_update_dpp(0, xi, 0x128, 0xf, 0xf, false));  // row_ror:8
+  if (m == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if (m == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  return x + shfl_xor(x, m);
+}
+
+// max(x, x[lane ^ m]) for m = 16 or 32 through the permlane swaps (bit-identical to the shuffle form), else a shuffle.
+__device__ __forceinline__ float xor_max(float x, int m) {
+  if (m == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  if (m == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  return fmaxf(x, shfl_xor(x, m));
+}
+
 }  // namespace gdr

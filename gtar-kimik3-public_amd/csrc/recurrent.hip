@@ -44,14 +44,6 @@ __device__ __forceinline__ void rank1_update(float4& s, float kr, float u0, floa
   s.z = __builtin_fmaf(kr, u2, s.z); s.w = __builtin_fmaf(kr, u3, s.w);
 }
 
-// x[l] + x[l ^ 32] in every lane l, through v_permlane32_swap (gfx950): with both operands x, the first result
-// holds the lower half's values in both halves and the second the upper half's, so the sum is formed in the same
-// order in every lane.
-__device__ __forceinline__ float half_swap_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // q, k and v share one element type InT (bf16 or fp32; the host widens mixed or fp16 inputs to fp32, exactly), so
 // every load has a static type and the compiler can track each one's completion precisely.
 // The body of the decode kernel and of the verify kernel (kRecord: also store each token's update row).  With
@@ -279,7 +271,7 @@ __device__ __forceinline__ void recurrent_body(const gdr_args& a, int n_slices, 
       float p = 0.f;
       for (int c = lane; c < K; c += kWave) p += s_q[tt][c] * s_k[tt][c];
 #pragma unroll
-      for (int m = 1; m < kWave; m *= 2) p += shfl_xor(p, m);
+      for (int m = 1; m < kWave; m *= 2) p = xor_sum(p, m);
       if (lane == 0) s_qk[tt] = p;
     }
     for (int tt = 0; tt < n_tok; ++tt) {
@@ -308,13 +300,8 @@ __device__ __forceinline__ void recurrent_body(const gdr_args& a, int n_slices, 
       for (int m = NQ; m < kWave; m *= 2) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          if (m == 32) {  // across the wave halves: a VALU lane swap, no LDS round trip
-            ak[j] = half_swap_sum(ak[j]);
-            aq[j] = half_swap_sum(aq[j]);
-          } else {
-            ak[j] += shfl_xor(ak[j], m);
-            aq[j] += shfl_xor(aq[j], m);
-          }
+          ak[j] = xor_sum(ak[j], m);  // VALU lane moves for m = 8, 16, 32: no LDS round trip
+          aq[j] = xor_sum(aq[j], m);
         }
       }
       if (lane < NQ) {
