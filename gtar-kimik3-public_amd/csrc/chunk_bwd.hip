@@ -26,6 +26,8 @@
 // Launches: the forward record and a state recompute (chunk_split.hip, states mode), then here
 //   chunk_dscan_kernel   reverse scan over chunks with dS in registers; writes dS' (bf16) per chunk and du^T
 //   chunk_dlocal_kernel  per (chunk, head): everything chunk-local, including the products with S and dS'
+#include <type_traits>
+
 #include "chunk_common.h"
 #include "gdr_internal.h"
 #include "split_common.h"
@@ -36,7 +38,9 @@ using namespace chunk;
 
 namespace {
 
-constexpr int kDScanThreads = 512;  // 4 compute waves of 16 value columns + 4 DMA loader waves
+// Threads of a reverse-scan workgroup of SL value columns: SL / 16 compute waves of 16 columns + 4 DMA loader waves.
+template <int SL>
+constexpr int dscan_threads() { return 64 * (SL / 16 + 4); }
 
 // Position of the 4-channel block [c, c + 4) (c % 4 == 0) in a row of the permuted W / Q e^B record layout:
 // within a 32-channel group, channel 4 g + j sits at 8 g + j and channel 16 + 4 g + j at 8 g + 4 + j.
@@ -45,24 +49,29 @@ __device__ __forceinline__ int perm_pos(int c) { return (c & ~31) + 8 * ((c & 15
 __device__ __forceinline__ bf16x8 ld8(const __bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ bf16x4 ld4(const __bf16* p) { return *reinterpret_cast<const bf16x4*>(p); }
 
-// ============================ reverse state scan: one workgroup per (sequence, head) x 64 columns ============================
+// ============================ reverse state scan: one workgroup per (sequence, head) x SL columns ============================
 // Per chunk c (last to first), each compute wave holds dS' = dS_{c+1} for 16 value columns in registers:
 //   du = Sc^T dO + Kt dS'  (row blocks i: Kt rows on 16x16x32 MFMAs with dS' as the two-tile B operand, Sc^T tiles
 //   and dO blocks through the transposing LDS read on 16x16x16 MFMAs), then
 //   dS = diag(gamma) dS' + Qd^T dO - W^T du  (Qd^T, W^T read transposed from the permuted record rows).
 // The loader waves stream the next record (W, Q e^B, Kt, Sc, gamma) and the dO slice into the other LDS buffer.
-template <int VARIANT, int K>
-__global__ __launch_bounds__(kDScanThreads, 1) void chunk_dscan_kernel(const gdr_args a, const gdr_grads g, int n_slices,
-                                                                       int xcd_map, int nc, int64_t rec_bytes,
-                                                                       const unsigned char* __restrict__ rec_ws,
-                                                                       __bf16* __restrict__ dstates,
-                                                                       __bf16* __restrict__ dubt) {
+// SL (64, 32 or 16 columns) is chosen per launch as for the forward scan: every compute wave reads the whole record
+// from LDS each step, so narrower slices mean fewer waves per CU sharing its LDS bandwidth and more CUs at work.
+template <int VARIANT, int K, int SL>
+__global__ __launch_bounds__(dscan_threads<SL>(), 1) void chunk_dscan_kernel(const gdr_args a, const gdr_grads g,
+                                                                             int n_slices, int xcd_map, int nc,
+                                                                             int64_t rec_bytes,
+                                                                             const unsigned char* __restrict__ rec_ws,
+                                                                             __bf16* __restrict__ dstates,
+                                                                             __bf16* __restrict__ dubt) {
   constexpr bool kDelta = VARIANT != GDR_GLA;
   constexpr int KT = K / 16, KS = K / 32;
   using R = Rec<K>;
-  constexpr int DO = R::FIX;                           // dO slice: bf16 [64][64], 16-byte chunks swizzled by row
-  constexpr int SB = R::FIX + kChunk * kScanSlice * 2;  // LDS bytes per buffer
-  constexpr int NF = R::FIX / 16, NDO = kChunk * kScanSlice * 2 / 16;
+  constexpr int kComp = SL / 16;                // compute waves
+  constexpr int CPR = SL / 8;                   // 16-byte chunks per dO row
+  constexpr int DO = R::FIX;                    // dO slice: bf16 [64][SL], chunk q of row r at slot q ^ (r % CPR)
+  constexpr int SB = R::FIX + kChunk * SL * 2;  // LDS bytes per buffer
+  constexpr int NF = R::FIX / 16, NDO = kChunk * SL * 2 / 16;
   constexpr int G0 = kDelta ? 0 : R::QD / 1024;        // GLA reads no W: its copies start at Q e^B
   constexpr int NG = ((NF + NDO + 63) / 64 - G0 + 3) / 4;  // 64-piece groups per loader wave
   extern __shared__ __align__(16) unsigned char smem[];
@@ -79,12 +88,12 @@ __global__ __launch_bounds__(kDScanThreads, 1) void chunk_dscan_kernel(const gdr
   }
   const int H = a.heads, V = a.value_dim, len = a.seq_len;
   const int n = bh / H, h = bh % H;
-  const int v0 = slice * kScanSlice;
+  const int v0 = slice * SL;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
 
-  if (wave >= 4) {
+  if (wave >= kComp) {
     // ---------------- loader waves ----------------
-    const int lw = wave - 4;
+    const int lw = wave - kComp;
     const unsigned char* rec0 = rec_ws + (int64_t(n) * nc * H + h) * rec_bytes;
     const int64_t rec_stride = int64_t(H) * rec_bytes;
     const __bf16* dop = static_cast<const __bf16*>(g.d_out.ptr) + n * g.d_out.stride_b + h * g.d_out.stride_h;
@@ -100,7 +109,7 @@ __global__ __launch_bounds__(kDScanThreads, 1) void chunk_dscan_kernel(const gdr
           if (idx < NF) {
             from = src + idx * 16;
           } else {
-            const int p = idx - NF, row = p >> 3, q = (p & 7) ^ (row & 7);  // stored slot p & 7 holds chunk q
+            const int p = idx - NF, row = p / CPR, q = (p % CPR) ^ (row % CPR);  // slot p % CPR holds chunk q
             const int t = min(c * kChunk + row, len - 1);                   // clamped rows meet zero Qd/Sc rows
             from = dop + int64_t(t) * g.d_out.stride_t + v0 + 8 * q;
           }
@@ -152,7 +161,7 @@ __global__ __launch_bounds__(kDScanThreads, 1) void chunk_dscan_kernel(const gdr
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 16 * i + 4 * g4 + (l16 >> 2), col = lc0 + 4 * (l16 & 3);
-      dob[i] = lds_read_tr(smem, boff + DO + 2 * (row * kScanSlice + (((col >> 3) ^ (row & 7)) << 3) + (col & 7)));
+      dob[i] = lds_read_tr(smem, boff + DO + 2 * (row * SL + (((col >> 3) ^ (row % CPR)) << 3) + (col & 7)));
     }
 
     // du_i = Kt_i dS' + sum_{i' >= i} Sc_{i'i}^T dO_{i'}
@@ -1015,20 +1024,30 @@ hipError_t launch_bwd_typed(const gdr_args& a, const gdr_grads& g, const BwdLayo
   const int nc = (a.seq_len + kChunk - 1) / kChunk;
   const int bh = a.batch * a.heads;
   const int64_t rec = Rec<K>::bytes(a.value_dim);
-  constexpr int dscan_lds = 2 * (Rec<K>::FIX + kChunk * kScanSlice * 2);
   constexpr int dlocal_lds = DLocalLds<K>::BYTES;
-  hipError_t e = configure_lds<&chunk_dscan_kernel<VARIANT, K>>(dscan_lds);
-  if (e == hipSuccess) e = configure_lds<&chunk_dlocal_kernel<VARIANT, K>>(dlocal_lds);
+  hipError_t e = configure_lds<&chunk_dlocal_kernel<VARIANT, K>>(dlocal_lds);
   if (e != hipSuccess) return e;
   if (nc == 0) return hipSuccess;
   const __bf16* states = reinterpret_cast<const __bf16*>(ws + Lw.states);
   __bf16* dstates = reinterpret_cast<__bf16*>(ws + Lw.dstates);
   const __bf16* ubuf = reinterpret_cast<const __bf16*>(ws + Lw.ubuf);
   __bf16* dubt = reinterpret_cast<__bf16*>(ws + Lw.dubt);
-  const int n_slices = a.value_dim / kScanSlice;
   const int xcd_map = (bh % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((chunk_dscan_kernel<VARIANT, K>), dim3(bh * n_slices), dim3(kDScanThreads), dscan_lds, stream,
-                     a, g, n_slices, xcd_map, nc, rec, ws + Lw.rec, dstates, dubt);
+  auto dscan = [&](auto sl_c) -> hipError_t {
+    constexpr int SL = decltype(sl_c)::value;
+    constexpr int lds = 2 * (Rec<K>::FIX + kChunk * SL * 2);
+    constexpr auto kernel = &chunk_dscan_kernel<VARIANT, K, SL>;
+    const hipError_t err = configure_lds<kernel>(lds);
+    if (err != hipSuccess) return err;
+    const int n_slices = a.value_dim / SL;
+    hipLaunchKernelGGL(kernel, dim3(bh * n_slices), dim3(dscan_threads<SL>()), lds, stream, a, g, n_slices, xcd_map,
+                       nc, rec, ws + Lw.rec, dstates, dubt);
+    return hipSuccess;
+  };
+  const int sl = scan_slice(bh, a.value_dim);
+  e = sl == 64 ? dscan(std::integral_constant<int, 64>{})
+               : sl == 32 ? dscan(std::integral_constant<int, 32>{}) : dscan(std::integral_constant<int, 16>{});
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((chunk_dlocal_kernel<VARIANT, K>), dim3(bh * nc), dim3(64 * DLocalLds<K>::NW), dlocal_lds,
                      stream, a, g, nc, states, dstates, ubuf, dubt);
   return hipGetLastError();

@@ -1174,6 +1174,8 @@ hipError_t launch_prep(const gdr_args& a, const gdr_prologue& pro, hipStream_t s
   return hipGetLastError();
 }
 
+}  // namespace
+
 // Compute units of the current device (queried once per device; 256 on MI355X).
 int device_cus() {
   constexpr int kMaxDevices = 64;
@@ -1196,6 +1198,8 @@ int scan_slice(int64_t bh, int value_dim) {
     if (value_dim % sl == 0 && bh * (value_dim / sl) >= cus) return sl;
   return 16;
 }
+
+namespace {
 
 template <int VARIANT, int K, typename OutT, int SL, int NT, int kMode, typename T>
 hipError_t launch_scan_sl(const gdr_args& a, int nc, __bf16* states, __bf16* ubuf, hipStream_t stream) {

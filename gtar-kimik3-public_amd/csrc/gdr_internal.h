@@ -43,6 +43,10 @@ hipError_t launch_short_conv(const gdr_conv_args& a, hipStream_t stream);
 // The layer's output epilogue (RMSNorm x SiLU gate); arguments validated.
 hipError_t launch_norm_gate(const gdr_norm_gate_args& a, hipStream_t stream);
 
+// Value columns per state-scan workgroup (forward and reverse): the widest of 64 and 32 whose workgroups, bh
+// (sequence, head) pairs times value_dim / width, still cover every CU of the current device, else 16.
+int scan_slice(int64_t bh, int value_dim);
+
 // `pro` is the fused layer prologue (flags 0 for the plain op).
 int64_t chunk_workspace_bytes(const gdr_args& a);
 hipError_t launch_chunk_split(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream);

@@ -7,8 +7,6 @@
 namespace gdr {
 namespace chunk {
 
-constexpr int kScanSlice = 64;  // value columns per reverse-scan (backward) workgroup
-
 // Workspace record of one (chunk, head); byte offsets.  UT (U^T, [V][64]) closes the record.  Rows are unpadded;
 // 16-byte chunks are XOR-swizzled within a row instead (chunk c of row r stored at chunk c ^ (r mod chunks per
 // row)), which keeps every LDS read pattern of the scan kernel free of bank conflicts.
