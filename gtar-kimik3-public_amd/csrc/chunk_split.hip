@@ -483,10 +483,14 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
   // ---- 3a. channel vectors, spread over the workgroup: EPRE[i] = e^{a_{i-1}}, ETAIL[i] = e^{B_end - a_i};
   // strip key factors RDS[i] = e^{-T_i} (0 for a hot channel) and FAR = e^{a_{i-1} - a_j} for tiles (2,0),
   // (3,0), (3,1) ----
+  // Thread x covers channel x mod K of the vectors v = x / K, x / K + 256 / K, ... (15 vectors of K channels), so it
+  // reads that channel's four block totals once.
+  static_assert(256 % K == 0, "channel vectors: a thread keeps one channel");
   if constexpr (kGate) {
-    for (int idx = threadIdx.x; idx < 15 * K; idx += 256) {
-      const int v = idx / K, ch = idx % K;
-      const float t0 = tot[ch], t1 = tot[K + ch], t2 = tot[2 * K + ch], t3 = tot[3 * K + ch];
+    const int ch = threadIdx.x % K;
+    const float t0 = tot[ch], t1 = tot[K + ch], t2 = tot[2 * K + ch], t3 = tot[3 * K + ch];
+#pragma unroll
+    for (int v = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / K); v < 15; v += 256 / K) {  // wave-uniform v
       if (v < 4) {
         const float t = v == 0 ? t0 : v == 1 ? t1 : v == 2 ? t2 : t3;
         rds[v * K + ch] = -t > kHot ? 0.f : __builtin_amdgcn_exp2f(-t);
@@ -500,11 +504,9 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
         etail_v[i * K + ch] = __builtin_amdgcn_exp2f(i == 0 ? t1 + t2 + t3 : i == 1 ? t2 + t3 : i == 2 ? t3 : 0.f);
       }
     }
-  }
-  if (threadIdx.x < K) {
-    const int ch = threadIdx.x;
-    const float b_end = kGate ? tot[ch] + tot[K + ch] + tot[2 * K + ch] + tot[3 * K + ch] : 0.f;
-    reinterpret_cast<float*>(rec + R::GAM)[ch] = kGate ? __builtin_amdgcn_exp2f(b_end) : 1.f;
+    if (threadIdx.x < K) reinterpret_cast<float*>(rec + R::GAM)[ch] = __builtin_amdgcn_exp2f(t0 + t1 + t2 + t3);
+  } else {
+    if (threadIdx.x < K) reinterpret_cast<float*>(rec + R::GAM)[threadIdx.x] = 1.f;
   }
   lds_barrier();
 
