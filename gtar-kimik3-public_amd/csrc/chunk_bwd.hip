@@ -252,9 +252,9 @@ struct DLocalLds {
   static constexpr int TOT = 4 * RB;            // fp32 [4][K] block totals of the block-local log2-gate cumsum
   static constexpr int BETA = TOT + 4 * K * 4;  // fp32 [64]
   static constexpr int HOT = BETA + 256;        // u8 [4][K] channels whose block span exceeds kDiagSpan
-  static constexpr int DB = HOT + 4 * K;        // fp32 [NW][64] per-wave dbeta partials
+  static constexpr int DB = HOT + 4 * K;        // fp32 [3][NW][64] per-wave dbeta partials, one slot per term
   static constexpr int BP = K + 4;              // fp32 pitch of BB
-  static constexpr int BB = DB + NW * 256;      // fp32 [64][BP] block-local log2-gate cumsum (row-owned scan)
+  static constexpr int BB = DB + 3 * NW * 256;  // fp32 [64][BP] block-local log2-gate cumsum (row-owned scan)
   static constexpr int kPre = 2;                // value passes whose dO, u and du^T are fetched at the start
   static constexpr int DOU = BB + 64 * BP * 4;  // [kPre][dO, u, du^T] swizzled pass buffers, filled by LDS DMA
   static constexpr int BYTES = DOU + kPre * 3 * PB;
@@ -298,6 +298,22 @@ __device__ __forceinline__ void store_grad4(const gdr_tensor& t, int64_t off, fl
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) store_grad(t, off + r, v[r]);
+}
+
+// Element off + r * stride of a gradient tensor for the rows r < min(4, rows) (rows may be <= 0): the dtype test once.
+__device__ __forceinline__ void store_rows4(const gdr_tensor& t, int64_t off, int64_t stride, const float (&v)[4],
+                                            int rows) {
+  if (t.dtype == GDR_F32) {
+    float* p = static_cast<float*>(const_cast<void*>(t.ptr)) + off;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (r < rows) p[r * stride] = v[r];
+  } else {
+    __bf16* p = static_cast<__bf16*>(const_cast<void*>(t.ptr)) + off;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (r < rows) p[r * stride] = bf(v[r]);
+  }
 }
 
 // Byte offset of (row, col) in a swizzled bf16 [64][64] pass buffer: 16-byte chunk q of row r sits at chunk q ^ (r % 8).
@@ -762,8 +778,11 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
   // ---- 5. dSc = tril(dO u^T) and dP = diag(beta) dL (bf16) into R4; dbeta partials into this wave's DB row ----
   __bf16* DSCL = reinterpret_cast<__bf16*>(smem + L::R4);
   __bf16* DPL = DSCL + 64 * DP;
+  // dbeta partials of this wave, each row written once per term: rowsum(dL (x) P) at DB[t], rowsum(X2 (x) V) at
+  // DB[64 NW + t], rowsum(X1 (x) K e^B) at DB[128 NW + t] (rows this wave does not reach stay zero)
   float* DB = reinterpret_cast<float*>(smem + L::DB) + 64 * w;
   DB[lane] = 0.f;
+  DB[64 * NW + lane] = 0.f;
 #pragma unroll
   for (int ii = 0; ii < NRT; ++ii)
 #pragma unroll
@@ -774,12 +793,12 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
         const float dlv = t > s ? -dl[ii][r] : 0.f;
         DPL[t * DP + s] = bf(BETA[t] * dlv);
         const float v = sum16(dlv * pv[ii][r]);  // rowsum(dL (x) P) over this wave's 16 columns
-        if (l16 == 0) DB[t] += v;
+        if (l16 == 0) DB[t] = v;
       }
     }
   if constexpr (kDelta) {
     const float v = sum_groups(dbv);  // rowsum(X2 (x) V) over this wave's value tiles
-    if (g4 == 0) DB[16 * tb + l16] += v;
+    if (g4 == 0) DB[64 * NW + 16 * tb + l16] = v;
   }
   bnd = sum_groups(bnd);
   lds_barrier();
@@ -900,6 +919,8 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
       }
     }
     // assembly of row tile i
+    float dq4[4], dk4[4];
+    const float4 b4 = kDelta ? *reinterpret_cast<const float4*>(BETA + 16 * i + 4 * g4) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * i + 4 * g4 + r;
@@ -907,7 +928,7 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
       const float qv = f32(qc[i][r]), kv = f32(kc[i][r]);
       const float dqv = scale * (qd[i][r] * eb + lq[r]);
       const float x1v = kDelta ? -x1[i][r] : 0.f;  // X1 = -X2 S^T
-      const float bt = kDelta ? BETA[t] : 0.f;
+      const float bt = r == 0 ? b4.x : r == 1 ? b4.y : r == 2 ? b4.z : b4.w;
       const float dkp = bt * eb * x1v + lp[r];       // the e^{+B} roles
       const float dkn = scale * kq[r] + kp2[r];      // the e^{-B} roles
       const float dktr = kt[i][r] * ex2(bend - bc[i][r]);
@@ -915,13 +936,14 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
       ktv[i][r] = kv * dktr;
       if constexpr (kDelta) {
         const float v = sum16(x1v * kv * eb);  // rowsum(X1 (x) K e^B) over this wave's channels
-        if (l16 == 0) DB[t] += v;
+        if (l16 == 0) DB[128 * NW + t] = v;
       }
-      if (t < nvalid) {
-        store_grad(g.d_query, qrow0 + int64_t(t0 + t) * g.d_query.stride_t, dqv);
-        store_grad(g.d_key, krow0 + int64_t(t0 + t) * g.d_key.stride_t, dkp + dkn + dktr);
-      }
+      dq4[r] = dqv;
+      dk4[r] = dkp + dkn + dktr;
     }
+    const int t4 = 16 * i + 4 * g4;  // the lane's four rows t4 .. t4 + 3, one dtype branch per tensor
+    store_rows4(g.d_query, qrow0 + int64_t(t0 + t4) * g.d_query.stride_t, g.d_query.stride_t, dq4, nvalid - t4);
+    store_rows4(g.d_key, krow0 + int64_t(t0 + t4) * g.d_key.stride_t, g.d_key.stride_t, dk4, nvalid - t4);
   }
 
   // ---- 7. gate gradient: inclusive suffix over rows of the non-Kt terms + e^{B_end} rowsum(S (x) dS') + exclusive
@@ -985,7 +1007,7 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
       const float* DBA = reinterpret_cast<const float*>(smem + L::DB);
       float v = 0.f;
 #pragma unroll
-      for (int q = 0; q < NW; ++q) v += DBA[q * 64 + tid];
+      for (int q = 0; q < NW; ++q) v += DBA[q * 64 + tid] + DBA[(NW + q) * 64 + tid] + DBA[(2 * NW + q) * 64 + tid];
       float* dbp = static_cast<float*>(const_cast<void*>(g.d_beta.ptr)) + n * g.d_beta.stride_b + h * g.d_beta.stride_h;
       dbp[int64_t(t0 + tid) * g.d_beta.stride_t] = v;
     }
