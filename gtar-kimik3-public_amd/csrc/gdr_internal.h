@@ -35,8 +35,6 @@ hipError_t launch_commit_verify(const gdr_args& prev, const float* prev_updates,
 // Enqueue the chunkwise forward; `a` has been validated (q, k, v share one dtype).
 hipError_t launch_chunk(const gdr_args& a, hipStream_t stream);
 
-// Chunkwise forward as a chunk-parallel preparation launch plus a state-scan launch over a workspace of
-// chunk_workspace_bytes(a) bytes at a.workspace.
 // Causal grouped-query attention and the segment-aware short convolution; arguments validated.
 hipError_t launch_attention(const gdr_attention_args& a, hipStream_t stream);
 hipError_t launch_short_conv(const gdr_conv_args& a, hipStream_t stream);
@@ -47,7 +45,8 @@ hipError_t launch_norm_gate(const gdr_norm_gate_args& a, hipStream_t stream);
 // (sequence, head) pairs times value_dim / width, still cover every CU of the current device, else 16.
 int scan_slice(int64_t bh, int value_dim);
 
-// `pro` is the fused layer prologue (flags 0 for the plain op).
+// Chunkwise forward as a chunk-parallel preparation launch plus a state-scan launch over a workspace of
+// chunk_workspace_bytes(a) bytes at a.workspace; `pro` is the fused layer prologue (flags 0 for the plain op).
 int64_t chunk_workspace_bytes(const gdr_args& a);
 hipError_t launch_chunk_split(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream);
 
