@@ -14,8 +14,11 @@
 //     straight from the score registers as B (the key order inside a 32-key step is the one the score tiles give;
 //     the V^T read follows it), so O^T lands in the same per-query-row lane layout.
 // Scores are exponentiated with v_exp_f32 in log2 units (the scale folded into one FMA); only tiles crossing the
-// diagonal or the sequence end are masked, and the accumulators are rescaled only when a running max moved (uniform
-// branches around VALU work; no MFMA sits under a data-dependent branch).
+// diagonal or the sequence end are masked.  The exponent base of a row moves only when a tile's max exceeds it by
+// more than 2^8 (probabilities stay below 256, exact in bf16/f16 range), so the accumulators are rescaled on a few
+// tiles only, and the row sums come out of the MFMA (all-ones A operand) from the same rounded probabilities as
+// P V (uniform branches around VALU work; no MFMA sits under a data-dependent branch).  K tiles run one ahead of V
+// tiles, so each tile's exponentials interleave with the next tile's score MFMAs in one basic block.
 #include "chunk_common.h"
 #include "gdr_internal.h"
 
@@ -32,6 +35,7 @@ constexpr int kBN = 64;   // keys per LDS tile
 constexpr int kAttnThreads = 256;
 constexpr int kRB = 2;  // 16-row query blocks per wave
 constexpr float kNegInf = -__builtin_inff();
+constexpr float kLazy = 8.f;  // log2 of the largest probability before the accumulators are rebased
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -128,60 +132,84 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
 
   // ---- key/value tiles: global -> LDS directly (global_load_lds_dwordx4: a lane's 16 bytes land at the wave-
   // uniform LDS base + 16 * lane).  Row r, chunk c of a tile is stored at chunk c ^ (r mod DC), so each lane loads
-  // the global chunk that belongs at its LDS slot. ----
+  // the global chunk that belongs at its LDS slot.  K runs one tile ahead of V: the score MFMAs of tile kb + 1 are
+  // issued beside the softmax of tile kb, which has no dependence on them. ----
   const int kend = min(len, q0 + kBM);  // keys this block can see
   const int nkb = (kend + kBN - 1) / kBN;
-  constexpr int GROUPS = kBN * DC / kWave;  // 64-piece groups per tile
+  constexpr int GROUPS = kBN * DC / kWave;  // 64-piece groups per K or V tile
   constexpr int kWaves = kAttnThreads / kWave;
-  static_assert((2 * GROUPS) % kWaves == 0, "tile groups per wave");
-  auto issue_tile = [&](int kb, int buf) {
+  constexpr int GPW = GROUPS / kWaves;      // groups per wave per tile
+  static_assert(GROUPS % kWaves == 0, "tile groups per wave");
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);
+  int lrow[GPW], lcol[GPW];      // this lane's tile row and global 16-byte chunk, per group
+  int64_t koffs[GPW], voffs[GPW];  // ... as element offsets from the tile's first key row
 #pragma unroll
-    for (int k = 0; k < 2 * GROUPS / kWaves; ++k) {
-      const int g = wave + kWaves * k;
-      const bool is_v = g >= GROUPS;
-      const int gg = is_v ? g - GROUPS : g;
-      const int slot = kWave * gg + lane, row = slot / DC, cc = (slot % DC) ^ (row % DC);
-      const int64_t key = min(kb * kBN + row, len - 1);
-      const T* src = is_v ? vp + key * a.v.stride_t + 8 * cc : kp + key * a.k.stride_t + 8 * cc;
-      T* dst = (is_v ? vs : ks) + buf * TILE + kWave * 8 * gg;
-      lds_dma16(src, dst);
+  for (int k = 0; k < GPW; ++k) {
+    const int slot = kWave * (uwave + kWaves * k) + lane;
+    lrow[k] = slot / DC;
+    lcol[k] = (slot % DC) ^ (lrow[k] % DC);
+    koffs[k] = int64_t(lrow[k]) * a.k.stride_t + 8 * lcol[k];
+    voffs[k] = int64_t(lrow[k]) * a.v.stride_t + 8 * lcol[k];
+  }
+  // Rows past the sequence end (last tile only) read the last key row instead; the mask removes them.
+  auto issue = [&](const T* base, int64_t stride, const int64_t (&offs)[GPW], T* tile, int kb) {
+    const T* tb = base + int64_t(kb) * kBN * stride;
+    const int lim = len - 1 - kb * kBN;
+    if (lim >= kBN - 1) {
+#pragma unroll
+      for (int k = 0; k < GPW; ++k) lds_dma16(tb + offs[k], tile + kWave * 8 * (uwave + kWaves * k));
+    } else {
+#pragma unroll
+      for (int k = 0; k < GPW; ++k)
+        lds_dma16(tb + int64_t(min(lrow[k], lim)) * stride + 8 * lcol[k], tile + kWave * 8 * (uwave + kWaves * k));
     }
   };
 
+  // This lane's LDS element offsets inside a tile: the K fragment of k step ds (row block 0), and the V^T fragment
+  // of output column tile t (key rows 4 g4 + (l16 >> 2) + {0, 16, 32, 48}: the swizzle is the same for all four).
+  int koff[DS], voff[DT];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) koff[ds] = l16 * D + (((4 * ds + g4) ^ (l16 % DC)) << 3);
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    const int col = 16 * t + 4 * (l16 & 3), r0 = 4 * g4 + (l16 >> 2);
+    voff[t] = r0 * D + (((col >> 3) ^ (r0 % DC)) << 3) + (col & 7);
+  }
+
   const float c = a.scale * kLog2e;  // scores in log2 units
-  float m[kRB], l[kRB];               // running max (log2 units) and sum of this lane's query rows
-  floatx4 o[kRB][DT];
+  // Per lane and row block: m is the exponent base (log2 units) of the probabilities accumulated so far; it only
+  // moves when a tile's row max exceeds it by more than kLazy, so every probability stays below 2^kLazy and the
+  // accumulators are rescaled on a few tiles only.  lsum accumulates the row sums of the same bf16/f16
+  // probabilities the P V products use (an all-ones A operand on the MFMA; every element of lsum[b] holds the sum).
+  float m[kRB], mx[kRB];
+  floatx4 o[kRB][DT], lsum[kRB];
 #pragma unroll
   for (int b = 0; b < kRB; ++b) {
     m[b] = kNegInf;
-    l[b] = 0.f;
+    lsum[b] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[b][t] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
+  V8 ones;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ones[i] = static_cast<T>(1.f);
 
-  issue_tile(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {  // the accumulators start at zero right before this loop
-    const int buf = kb & 1;
-    if (kb + 1 < nkb) issue_tile(kb + 1, buf ^ 1);  // every wave is done with that buffer (tile kb - 1)
-    const T* kt = ks + buf * TILE;
-
-    // S^T tiles: lane holds S[qpos[b]][kb * kBN + 16 t + 4 g4 + i]; each K fragment serves both row blocks
-    floatx4 s[kRB][4];
+  // S^T of the K tile at kt: lane holds S[qpos[b]][key0 + 16 t + 4 g4 + i]; each K fragment serves both row blocks.
+  auto scores = [&](const T* kt, floatx4 (&s)[kRB][4]) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int b = 0; b < kRB; ++b) s[b][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      const int row = 16 * t + l16;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
-        const V8 kf = *reinterpret_cast<const V8*>(kt + row * D + (((4 * ds + g4) ^ (row % DC)) << 3));
+        const V8 kf = *reinterpret_cast<const V8*>(kt + 16 * t * D + koff[ds]);
 #pragma unroll
         for (int b = 0; b < kRB; ++b) s[b][t] = M::run(kf, qf[b][ds], s[b][t]);
       }
     }
-    // Only a tile that crosses this wave's diagonal or the sequence end needs the causal mask (a uniform branch).
+  };
+  // Only a tile that crosses this wave's diagonal or the sequence end needs the causal mask (a uniform branch).
+  auto mask = [&](int kb, floatx4 (&s)[kRB][4]) {
     const bool full = (kb + 1) * kBN - 1 <= q0 + 32 * wave && (kb + 1) * kBN <= len;
     if (!full) {
 #pragma unroll
@@ -194,71 +222,111 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
             if (!(key <= qpos[b] && key < len)) s[b][t][i] = kNegInf;
           }
     }
-    float alpha[kRB];
-    V8 pf[kRB][2];
+  };
+  // Row max of one tile's raw scores, in log2 units.
+  auto rowmax = [&](const floatx4 (&s)[kRB][4]) {
 #pragma unroll
     for (int b = 0; b < kRB; ++b) {
-      float mx = kNegInf;  // of the raw scores; the scale c > 0 is applied once, inside the exponent's FMA
+      float x = kNegInf;  // the scale c > 0 is applied once, after the max
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[b][t][i]);
-      mx = xor_max(mx, 16);
-      mx = xor_max(mx, 32);
-      const float m_new = fmaxf(m[b], mx * c);
-      const float base = m_new == kNegInf ? 0.f : m_new;
-      alpha[b] = __builtin_amdgcn_exp2f(m[b] - base);
-      float rs = 0.f;
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          s[b][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[b][t][i], c, -base));
-          rs += s[b][t][i];
-        }
-      rs = xor_sum(rs, 16);
-      rs = xor_sum(rs, 32);
-      l[b] = l[b] * alpha[b] + rs;
-      m[b] = m_new;
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) pf[b][s2] = cat<V4, V8>(M::pack(s[b][2 * s2]), M::pack(s[b][2 * s2 + 1]));
+        for (int i = 0; i < 4; ++i) x = fmaxf(x, s[b][t][i]);
+      x = xor_max(x, 16);
+      x = xor_max(x, 32);
+      mx[b] = x * c;
     }
-
-    // O^T += V^T P^T: V^T rows 32 s2 + 4 g4 + r (and + 16), column 16 t + l16, through the transposing read; each
-    // V^T fragment serves both row blocks
-    // the running max moved for some lane: rescale the accumulators (alpha is exactly 1 where it did not)
+  };
+  // Moves the base of rows whose new max exceeds it by more than kLazy (a uniform branch per row block).
+  auto rebase = [&]() {
 #pragma unroll
     for (int b = 0; b < kRB; ++b) {
-      if (__any(alpha[b] != 1.f)) {
+      const bool move = mx[b] > m[b] + kLazy;  // false while both are -inf (no visible key yet)
+      if (__any(move)) {
+        const float alpha = move ? __builtin_amdgcn_exp2f(m[b] - mx[b]) : 1.f;  // 0 from a base of -inf
+        if (move) m[b] = mx[b];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lsum[b][i] *= alpha;
 #pragma unroll
         for (int t = 0; t < DT; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) o[b][t][i] *= alpha[b];
+          for (int i = 0; i < 4; ++i) o[b][t][i] *= alpha;
       }
     }
+  };
+  // Probabilities 2^(c s - m) of one tile as bf16/f16 MFMA operands.
+  auto probs = [&](floatx4 (&s)[kRB][4], V8 (&pf)[kRB][2]) {
+#pragma unroll
+    for (int b = 0; b < kRB; ++b) {
+      const float base = m[b] == kNegInf ? 0.f : m[b];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[b][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[b][t][i], c, -base));
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) pf[b][s2] = cat<V4, V8>(M::pack(s[b][2 * s2]), M::pack(s[b][2 * s2 + 1]));
+    }
+  };
+  // O^T += V^T P^T for the V tile at vt (bytes): V^T rows 32 s2 + 4 g4 + r (and + 16), column 16 t + l16, through
+  // the transposing read; each V^T fragment serves both row blocks.  Then the row sums.
+  auto pv = [&](const unsigned char* vt, const V8 (&pf)[kRB][2]) {
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const int col = 16 * t + 4 * (l16 & 3);
-        const int r0 = 32 * s2 + 4 * g4 + (l16 >> 2), r1 = r0 + 16;
-        const int off0 = buf * TILE + r0 * D + (((col >> 3) ^ (r0 % DC)) << 3) + (col & 7);
-        const int off1 = buf * TILE + r1 * D + (((col >> 3) ^ (r1 % DC)) << 3) + (col & 7);
-        const V4 lo = __builtin_bit_cast(V4, lds_read_tr(reinterpret_cast<const unsigned char*>(vs), off0 * 2));
-        const V4 hi = __builtin_bit_cast(V4, lds_read_tr(reinterpret_cast<const unsigned char*>(vs), off1 * 2));
+        const V4 lo = __builtin_bit_cast(V4, lds_read_tr(vt, 2 * (voff[t] + 32 * s2 * D)));
+        const V4 hi = __builtin_bit_cast(V4, lds_read_tr(vt, 2 * (voff[t] + (32 * s2 + 16) * D)));
         const V8 vf = cat<V4, V8>(lo, hi);
 #pragma unroll
         for (int b = 0; b < kRB; ++b) o[b][t] = M::run(vf, pf[b][s2], o[b][t]);
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile kb + 1 have landed
-    __syncthreads();                 // ... everyone's, and every wave is done with tile kb
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int b = 0; b < kRB; ++b) lsum[b] = M::run(ones, pf[b][s2], lsum[b]);
+  };
+  const unsigned char* vbytes = reinterpret_cast<const unsigned char*>(vs);
+
+  issue(kp, a.k.stride_t, koffs, ks, 0);
+  issue(vp, a.v.stride_t, voffs, vs, 0);
+  if (nkb > 1) issue(kp, a.k.stride_t, koffs, ks + TILE, 1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  floatx4 s[kRB][4];
+  scores(ks, s);
+  mask(0, s);
+  rowmax(s);
+  rebase();
+  __syncthreads();  // every wave has read K tile 0 before the first step refills its buffer
+  // Step kb: the probabilities of tile kb beside the score MFMAs of tile kb + 1, the P V MFMAs of tile kb, then the
+  // mask and row max of tile kb + 1 (one basic block up to the mask, so the VALU and MFMA work can interleave).
+  int kb = 0;
+  for (; kb + 1 < nkb; ++kb) {  // the accumulators start at zero right before this loop
+    const int cur = kb & 1;
+    // K tile kb (read in the previous step) and V tile kb - 1 are free
+    if (kb + 2 < nkb) issue(kp, a.k.stride_t, koffs, ks + cur * TILE, kb + 2);
+    issue(vp, a.v.stride_t, voffs, vs + (cur ^ 1) * TILE, kb + 1);
+    V8 pf[kRB][2];
+    probs(s, pf);
+    scores(ks + (cur ^ 1) * TILE, s);
+    pv(vbytes + cur * TILE * 2, pf);
+    mask(kb + 1, s);
+    rowmax(s);
+    rebase();
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of K tile kb + 2 and V tile kb + 1 have landed
+    __syncthreads();                 // ... everyone's, and every wave is done with K tile kb + 1 and V tile kb
+  }
+  {
+    V8 pf[kRB][2];
+    probs(s, pf);
+    pv(vbytes + (kb & 1) * TILE * 2, pf);
   }
 
 #pragma unroll
   for (int b = 0; b < kRB; ++b) {
     if (qpos[b] < len) {
-      const float inv = 1.f / l[b];
+      const float inv = 1.f / lsum[b][0];
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
         floatx4 y = o[b][t];

@@ -40,6 +40,27 @@ def test_attention_matches_exact_within_reference_bar(shape, dtype):
     assert out.dtype == dtype and err <= 2 * base + 1e-4
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("order", ["rising", "falling"])
+def test_attention_moving_row_maxima(dtype, order):
+    """Sharp softmax rows (scale 0.5 at D = 64) over keys whose norms rise (or fall) 8x along the sequence: with
+    rising norms each row's max keeps growing, so the exponent base moves many times, by small and large steps;
+    with falling norms it is set early and later probabilities are tiny.  Same bar as above."""
+    B, H, Hkv, T, D = 1, 4, 2, 700, 64
+    q, k, v = _qkv(B, H, Hkv, T, D, torch.float32, seed=8)
+    ramp = torch.linspace(0.25, 2.0, T).view(1, 1, T, 1)
+    k = k * (ramp if order == "rising" else ramp.flip(2))
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    exact = oracle.causal_attention(q, k, v, 0.5)
+    with torch.no_grad():
+        out = gdr.flash_attention(q.cuda(), k.cuda(), v.cuda(), softmax_scale=0.5)
+    sdpa = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True, scale=0.5)
+    err = (out.cpu().double() - exact).abs().max().item()
+    base = (sdpa.double() - exact).abs().max().item()
+    print(f"  {order} {dtype}: kernel {err:.2e}  sdpa {base:.2e}")
+    assert torch.isfinite(out).all() and err <= 2 * base + 1e-4
+
+
 def test_attention_packed_sequences_and_layer_layout():
     """cu_seqlens confines attention to each packed sequence (lengths around the 128-row block and 64-key tile
     edges, and a single token); q, k, v are the layer's transposed [B, T, H, D] views."""
