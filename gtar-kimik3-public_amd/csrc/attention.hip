@@ -27,7 +27,6 @@ namespace {
 
 using chunk::kLog2e;
 using chunk::lds_dma16;
-using chunk::lds_read_tr;
 using chunk::pack4;
 
 constexpr int kBM = 128;  // query rows per workgroup
@@ -39,6 +38,7 @@ constexpr float kLazy = 8.f;  // log2 of the largest probability before the accu
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short short4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
 struct Mma;
@@ -267,16 +267,36 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
       for (int s2 = 0; s2 < 2; ++s2) pf[b][s2] = cat<V4, V8>(M::pack(s[b][2 * s2]), M::pack(s[b][2 * s2 + 1]));
     }
   };
-  // O^T += V^T P^T for the V tile at vt (bytes): V^T rows 32 s2 + 4 g4 + r (and + 16), column 16 t + l16, through
-  // the transposing read; each V^T fragment serves both row blocks.  Then the row sums.
-  auto pv = [&](const unsigned char* vt, const V8 (&pf)[kRB][2]) {
+  // O^T += V^T P^T for the V tile at LDS byte address vt: V^T rows 32 s2 + 4 g4 + r (and + 16), column 16 t + l16,
+  // through the transposing read; each V^T fragment serves both row blocks.  Then the row sums.
+  // The reads are issued as inline assembly, one column tile ahead of their MFMAs, with their own lgkmcnt waits:
+  // the compiler cannot tell the transposing read from the key/value DMA still in flight into the other buffers,
+  // and would otherwise wait for that DMA (vmcnt(0)) before the first read.  LDS operations complete in order, so
+  // "lgkmcnt(4)" after the next tile's four reads covers this tile's reads whatever else the compiler interleaves.
+  auto pv = [&](uint32_t vt, const V8 (&pf)[kRB][2]) {
+    short4 x[2][4];
+    auto rd = [&](int t, short4 (&r)[4]) {
+      asm volatile(
+          "ds_read_b64_tr_b16 %0, %4\n\t"
+          "ds_read_b64_tr_b16 %1, %4 offset:%5\n\t"
+          "ds_read_b64_tr_b16 %2, %4 offset:%6\n\t"
+          "ds_read_b64_tr_b16 %3, %4 offset:%7"
+          : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+          : "v"(vt + 2 * voff[t]), "i"(2 * 16 * D), "i"(2 * 32 * D), "i"(2 * 48 * D));
+    };
+    rd(0, x[0]);
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
+      short4(&r)[4] = x[t & 1];
+      if (t + 1 < DT) {
+        rd(t + 1, x[(t + 1) & 1]);
+        asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+      } else {
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+      }
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const V4 lo = __builtin_bit_cast(V4, lds_read_tr(vt, 2 * (voff[t] + 32 * s2 * D)));
-        const V4 hi = __builtin_bit_cast(V4, lds_read_tr(vt, 2 * (voff[t] + (32 * s2 + 16) * D)));
-        const V8 vf = cat<V4, V8>(lo, hi);
+        const V8 vf = cat<V4, V8>(__builtin_bit_cast(V4, r[2 * s2]), __builtin_bit_cast(V4, r[2 * s2 + 1]));
 #pragma unroll
         for (int b = 0; b < kRB; ++b) o[b][t] = M::run(vf, pf[b][s2], o[b][t]);
       }
@@ -286,7 +306,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
 #pragma unroll
       for (int b = 0; b < kRB; ++b) lsum[b] = M::run(ones, pf[b][s2], lsum[b]);
   };
-  const unsigned char* vbytes = reinterpret_cast<const unsigned char*>(vs);
+  const uint32_t vlds = static_cast<uint32_t>((uintptr_t)(__attribute__((address_space(3))) const unsigned char*)vs);
 
   issue(kp, a.k.stride_t, koffs, ks, 0);
   issue(vp, a.v.stride_t, voffs, vs, 0);
@@ -310,7 +330,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
     V8 pf[kRB][2];
     probs(s, pf);
     scores(ks + (cur ^ 1) * TILE, s);
-    pv(vbytes + cur * TILE * 2, pf);
+    pv(vlds + cur * TILE * 2, pf);
     mask(kb + 1, s);
     rowmax(s);
     rebase();
@@ -320,7 +340,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
   {
     V8 pf[kRB][2];
     probs(s, pf);
-    pv(vbytes + (kb & 1) * TILE * 2, pf);
+    pv(vlds + (kb & 1) * TILE * 2, pf);
   }
 
 #pragma unroll
