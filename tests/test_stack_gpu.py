@@ -41,6 +41,35 @@ def test_stack_matches_oracle_on_packed_sequences():
         assert es <= 3e-2
 
 
+def test_stack_matches_oracle_at_head_dim_128():
+    """The production head size (KDA and attention heads of 128, grouped-query attention), a wider hidden size,
+    two stack layers of each kind (attention_interval 2) and sequence lengths around the 64-token chunk and
+    128-row attention block edges, against the fp64 oracle at the same bar."""
+    cfg = stack.StackConfig(hidden_size=256, intermediate_size=512, num_layers=4, num_attention_heads=4,
+                            num_key_value_heads=2, head_dim=128, kda_num_heads=2, kda_head_dim=128,
+                            attention_interval=2)
+    layers = stack.init_weights(cfg, seed=5)
+    lens = [1, 64, 129, 300]
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    T = int(cu[-1])
+    hidden = torch.randn(1, T, cfg.hidden_size, generator=torch.Generator().manual_seed(6)).bfloat16()
+    print(f"stack d128: {T} tokens", flush=True)
+    out, states = stack.HybridStack(cfg, layers).forward(hidden.cuda(), cu.cuda())
+    ref, ref_states = oracle.hybrid_stack(hidden, cu, layers, cfg)
+    delta, ref_delta = out.cpu().double() - hidden.double(), ref - hidden.double()
+    err = ((delta - ref_delta).abs().max() / ref_delta.abs().max()).item()
+    print(f"stack d128: residual-update err {err:.2e}")
+    assert err <= 5e-2
+    assert sum(r is None for r in ref_states) == 2  # two attention layers
+    for i, (s, r) in enumerate(zip(states, ref_states)):
+        if r is None:
+            assert s is None
+            continue
+        es = ((s.cpu().double() - r).norm() / r.norm()).item()
+        print(f"  layer {i} state err {es:.2e}")
+        assert es <= 3e-2
+
+
 def test_stack_full_shape_packed_equals_each_sequence_alone():
     """The packed-prefill configuration at its stated shape (hidden 1024, 16 x 128 heads, 3 KDA + 1 attention
     blocks, 32 sequences with lengths ~U[256, 4096]): the packed forward equals each sequence run on its own, to the
