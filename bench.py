@@ -576,7 +576,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=400,
+                    help="untimed prefill calls before the timed ones (about 0.1 s at c2): right after the inputs are "
+                         "built the GPU's clocks are still rising, and the first few tens of calls run up to 7 %% slower")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-verify", action="store_true", help="skip the speculative verify + commit leg")
