@@ -834,11 +834,12 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
 template <int SL, int NT>
 struct ScanShape {
   static constexpr int kCompute = SL / (16 * NT);                // compute waves, NT 16-column state tiles each
-  static constexpr int kLoaders = 4;                             // loader waves
-  static constexpr int kThreads = 64 * (kCompute + kLoaders);
+  // loader waves: in the output mode with at most two compute waves, enough for eight waves (two per SIMD), else
+  // four.  The record copy, not the arithmetic, sets the step's pace there.
+  static constexpr int loaders(int mode) { return mode == 0 && kCompute <= 2 ? 8 - kCompute : 4; }
   static constexpr int kOP = SL + 8;                             // row pitch (elements) of the output tile in LDS
   static constexpr int kStorers = 2;                             // kSave modes: waves storing the state / u tiles
-  static constexpr int threads(int mode) { return kThreads + (mode != 0 ? 64 * kStorers : 0); }
+  static constexpr int threads(int mode) { return 64 * (kCompute + loaders(mode)) + (mode != 0 ? 64 * kStorers : 0); }
 };
 
 // kMode: kScanOut writes the output (and the final state); kScanStates (the backward's recompute) instead writes the
@@ -856,7 +857,7 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::threads(kMode)), 1) void chunk_
   using V8 = vec8<T>;
   using V4 = vec4<T>;
   constexpr int kScanCompute = ScanShape<SL, NT>::kCompute, kOP = ScanShape<SL, NT>::kOP;
-  constexpr int kScanLoaders = ScanShape<SL, NT>::kLoaders;
+  constexpr int kScanLoaders = ScanShape<SL, NT>::loaders(kMode);
   using R = Rec<K>;
 
   constexpr int SB = R::FIX + R::ut_slice(SL);     // LDS bytes per buffer
