@@ -634,19 +634,19 @@ def main():
         "algorithmic_flops": flops,
     }
     if not opts.no_variants:
-        record["variants"] = bench_variants(gdr, workloads, torch, steps=20, warmup=5)
+        record["variants"] = bench_variants(gdr, workloads, torch, steps=50, warmup=200)
     if not opts.no_decode:
         record["decode"] = bench_decode(gdr, workloads, torch, warmup=20)
     if not opts.no_verify:
         record["verify"] = bench_verify(gdr, workloads, torch, warmup=10)
     if not opts.no_fused:
-        record["fused"] = bench_fused(gdr, torch, steps=20, warmup=5)
+        record["fused"] = bench_fused(gdr, torch, steps=20, warmup=100)
     if not opts.no_varlen:
-        record["varlen"] = bench_varlen(gdr, workloads, torch, steps=10, warmup=3)
+        record["varlen"] = bench_varlen(gdr, workloads, torch, steps=10, warmup=50)
     if not opts.no_stack:
         record["stack"] = bench_stack(gdr, workloads, torch, steps=5, warmup=2)
     if not opts.no_train:
-        record["train"] = bench_train(gdr, workloads, torch, steps=5, warmup=2)
+        record["train"] = bench_train(gdr, workloads, torch, steps=10, warmup=50)
     if opts.copy_mib:
         src = torch.ones(opts.copy_mib * 2**18, device="cuda")
         dst = torch.empty_like(src)
