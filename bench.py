@@ -21,6 +21,9 @@ One JSON line on stdout:
   * stack: the packed-prefill configuration through the hybrid stack harness (3 KDA blocks and 1 attention block
     of the 0.6B model's shapes, random bf16 weights, 32 sequences with lengths ~U[256, 4096]): end-to-end tokens/s
     and the KDA op's share of the time.
+  * attention: the stack's causal attention layer alone on the packed configuration (16 query / 8 key-value heads,
+    head dim 128, bf16): ms per call, TFLOP/s over the causal FLOPs 4 H D L (L + 1) / 2 per sequence, and the
+    fraction of dense bf16 MFMA peak.
   * train: the prefill configuration under torch.autograd, the training forward (gdr_chunk_fwd_train) then the
     backward (gdr_chunk_bwd_saved), steps queued back to back, with the backward's algorithmic bytes and HBM
     fraction.
@@ -417,6 +420,32 @@ def bench_varlen(gdr, workloads, torch, steps, warmup):
             "note": "KDA op only (the layer stack around it is out of scope)"}
 
 
+def bench_attention(gdr, workloads, torch, steps, warmup):
+    lengths = workloads.varlen_lengths(VARLEN["n_seqs"], VARLEN["low"], VARLEN["high"], seed=0)
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0).tolist()), dtype=torch.int32, device="cuda")
+    tokens, H, Hkv, D = int(cu[-1]), 16, 8, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(1, H, tokens, D, device="cuda", generator=g).bfloat16()
+    k, v = (torch.randn(1, Hkv, tokens, D, device="cuda", generator=g).bfloat16() for _ in range(2))
+    stream = torch.cuda.current_stream()
+    with torch.no_grad():
+        for _ in range(warmup):
+            gdr.flash_attention(q, k, v, cu_seqlens=cu)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            gdr.flash_attention(q, k, v, cu_seqlens=cu)
+        stop.record(stream)
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    flops = sum(4 * H * D * n * (n + 1) / 2 for n in lengths)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "packed_causal_attention", "n_seqs": len(lengths), "tokens": tokens, "heads": H,
+            "kv_heads": Hkv, "head_dim": D, "ms_per_call": round(ms, 4), "tflops": round(tflops, 1),
+            "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
 def bench_stack(gdr, workloads, torch, steps, warmup):
     stack = importlib.import_module("gtar-kimik3-public_amd.stack")
     cfg = stack.StackConfig()
@@ -584,6 +613,7 @@ def main():
     ap.add_argument("--no-verify", action="store_true", help="skip the speculative verify + commit leg")
     ap.add_argument("--no-fused", action="store_true", help="skip the fused-prologue prefill leg")
     ap.add_argument("--no-stack", action="store_true", help="skip the hybrid stack harness leg")
+    ap.add_argument("--no-attention", action="store_true", help="skip the packed attention leg")
     ap.add_argument("--no-varlen", action="store_true", help="skip the packed varlen prefill leg")
     ap.add_argument("--no-train", action="store_true", help="skip the forward + backward (autograd) leg")
     ap.add_argument("--no-variants", action="store_true", help="skip the GDN / GLA / DeltaNet variant sweep leg")
@@ -643,6 +673,8 @@ def main():
         record["fused"] = bench_fused(gdr, torch, steps=20, warmup=100)
     if not opts.no_varlen:
         record["varlen"] = bench_varlen(gdr, workloads, torch, steps=10, warmup=50)
+    if not opts.no_attention:
+        record["attention"] = bench_attention(gdr, workloads, torch, steps=10, warmup=20)
     if not opts.no_stack:
         record["stack"] = bench_stack(gdr, workloads, torch, steps=5, warmup=2)
     if not opts.no_train:
