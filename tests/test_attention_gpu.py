@@ -8,6 +8,8 @@ The short convolution is held to the fp64 oracle at 1e-2 relative to max |out| (
 the output, fp32 accumulation inside).
 """
 
+import importlib
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -80,6 +82,35 @@ def test_attention_packed_sequences_and_layer_layout():
         for s, e in zip(cu[:-1].tolist(), cu[1:].tolist()):
             alone = gdr.flash_attention(q[:, :, s:e].cuda(), k[:, :, s:e].cuda(), v[:, :, s:e].cuda())
             assert torch.equal(alone, out[:, :, s:e].contiguous()), (s, e)
+
+
+def test_attention_full_packed_shape_equals_each_sequence_alone():
+    """The stack's packed configuration at its stated shape (32 sequences with lengths ~U[256, 4096], 16 query /
+    8 key-value heads, head dim 128, bf16): the packed call equals each sequence run on its own bit for bit (the
+    tiles start at each sequence's first token either way), a property that holds at any size, so no fp64 oracle
+    has to run the full shape; the oracle bar is checked on the shortest sequence."""
+    workloads = importlib.import_module("gtar-kimik3-public_amd.workloads")
+    lengths = workloads.varlen_lengths(32, 256, 4096, seed=0)
+    cu = torch.tensor([0] + torch.tensor(lengths).cumsum(0).tolist(), dtype=torch.int32)
+    T, H, Hkv, D = int(cu[-1]), 16, 8, 128
+    print(f"attention full packed shape: {len(lengths)} seqs, {T} tokens", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    q = torch.randn(1, H, T, D, device="cuda", generator=gen).bfloat16()
+    k, v = (torch.randn(1, Hkv, T, D, device="cuda", generator=gen).bfloat16() for _ in range(2))
+    with torch.no_grad():
+        out = gdr.flash_attention(q, k, v, cu_seqlens=cu.cuda())
+        for s, e in zip(cu[:-1].tolist(), cu[1:].tolist()):
+            alone = gdr.flash_attention(q[:, :, s:e].contiguous(), k[:, :, s:e].contiguous(), v[:, :, s:e].contiguous())
+            assert torch.equal(alone, out[:, :, s:e].contiguous()), (s, e)
+    i = min(range(len(lengths)), key=lambda j: lengths[j])  # the shortest sequence, so the CPU check stays quick
+    s, e = int(cu[i]), int(cu[i + 1])
+    qs, ks, vs = (x[:, :, s:e].cpu() for x in (q, k, v))
+    exact = oracle.causal_attention(qs, ks, vs)
+    sdpa = F.scaled_dot_product_attention(qs, ks, vs, is_causal=True, enable_gqa=True)
+    err = (out[:, :, s:e].cpu().double() - exact).abs().max().item()
+    base = (sdpa.double() - exact).abs().max().item()
+    print(f"  sequence {i} ({e - s} tokens): kernel {err:.2e}  sdpa {base:.2e}")
+    assert err <= 2 * base + 1e-4
 
 
 def test_attention_scale_and_autocast():
