@@ -97,12 +97,17 @@ __global__ __launch_bounds__(dscan_threads<SL>(), 1) void chunk_dscan_kernel(con
     const unsigned char* rec0 = rec_ws + (int64_t(n) * nc * H + h) * rec_bytes;
     const int64_t rec_stride = int64_t(H) * rec_bytes;
     const __bf16* dop = static_cast<const __bf16*>(g.d_out.ptr) + n * g.d_out.stride_b + h * g.d_out.stride_h;
+    // Each slice workgroup of a head starts its copy at its own offset into the record, so that the slices do not
+    // request the same missing lines of the shared record at the same moment.
+    constexpr int kGroups = (NF + NDO + 63) / 64 - G0;
+    const int rot = (slice * kGroups) / n_slices;
     auto copy = [&](int c, int buf) {
       const unsigned char* src = rec0 + c * rec_stride;
       unsigned char* dst = smem + buf * SB;
 #pragma unroll
       for (int k = 0; k < NG; ++k) {
-        const int grp = G0 + lw + 4 * k;
+        const int j = lw + 4 * k;  // past the record: no copy
+        const int grp = j < kGroups ? G0 + (j + rot) % kGroups : 1 << 20;
         const int idx = 64 * grp + lane;
         if (idx < NF + NDO) {
           const void* from;

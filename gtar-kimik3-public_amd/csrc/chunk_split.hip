@@ -903,12 +903,18 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::threads(kMode)), 1) void chunk_
     const unsigned char* rec0 = ws + (int64_t(base) * H + h) * rec_bytes;
     const int64_t rec_stride = int64_t(H) * rec_bytes;
     const int ut_off = R::FIX + v0 * 64 * 2;
+    // The slice workgroups of one head read the same record lines.  Each starts its copy at its own offset into the
+    // record (slice / n_slices of the way through), so that a line is first requested by one slice and found in the
+    // XCD's L2 by the others later, instead of every slice asking for the same missing lines at the same moment.
+    constexpr int kGroups = (NF + NU + 63) / 64 - G0;  // 64-piece groups copied
+    const int rot = (slice * kGroups) / n_slices;
     auto copy_record = [&](int chunk, int buf) {
       const unsigned char* src = rec0 + chunk * rec_stride;
       unsigned char* dst = smem + buf * SB;
 #pragma unroll
       for (int k = 0; k < NG; ++k) {
-        const int g = G0 + lw + kScanLoaders * k;  // group of 64 16-byte pieces
+        const int j = lw + kScanLoaders * k;  // group of 64 16-byte pieces (past the record: no copy)
+        const int g = j < kGroups ? G0 + (j + rot) % kGroups : 1 << 20;
         const int idx = 64 * g + lane;
         if (idx < NF + NU) {
           const int off = idx < NF ? idx * 16 : ut_off + (idx - NF) * 16;
