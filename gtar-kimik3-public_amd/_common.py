@@ -5,8 +5,9 @@ gated_deltanet.py:472-520, gated_linear_attention.py:437-483, deltanet.py:399-44
   * scale = `scale or head_dim ** -0.5` (so 0.0 also selects the default, as in the reference),
   * the chunk path casts q, k, v to the autocast dtype when autocast is enabled (utils.py:84-88), and takes its
     matrix-product operands in k's dtype as the reference's kernels do (.to(k.dtype)): bf16 and f16 q, k, v run the
-    chunk kernels on bf16 / f16 MFMA operands, and fp32 q, k, v run the recurrent kernel over the whole sequence,
-    all in fp32 (the chunk backward takes bf16 only),
+    chunk kernels on bf16 / f16 MFMA operands; fp32 q, k, v run the recurrent kernel over the whole sequence, all in
+    fp32, when no gradient is needed; mixed fp32 / 16-bit q, k, v run on the 16-bit dtype; and a call that needs
+    gradients runs on bf16 operands whatever the input dtypes (the backward kernels are bf16),
   * a missing initial state is a zero fp32 state, a given one is used as `initial_state.float().contiguous()`,
   * the final state is always a fresh fp32 tensor and inputs are never modified,
   * the output has the value's dtype; `(out, final_state)` is returned only when `output_final_state`.
@@ -110,26 +111,25 @@ def run(variant: int, chunk: bool, query, key, value, gate, beta, scale, initial
             raise ValueError(f"{name}: initial_state must have shape {state_shape}, got {tuple(initial_state.shape)}")
         initial_state = initial_state.float().contiguous()
 
-    exact_f32 = chunk and any(x.dtype not in _OPERAND_DTYPES for x in (query, key, value))
-    if exact_f32:
+    if chunk and not grad and all(x.dtype == torch.float32 for x in (query, key, value)):
         # The reference's chunk kernels take their dot operands in the input dtype (.to(k.dtype),
         # kimi_delta_attention.py:99-100, :130, :135): fp32 inputs get fp32 products.  The chunk kernels multiply
         # 16-bit operands, so fp32 input runs the recurrence instead (every product and sum in fp32).
-        if grad:
-            raise NotImplementedError(f"{name}: fp32 q, k, v run the exact fp32 recurrence, which has no backward; "
-                                      "for training pass bfloat16 q, k, v (or run under torch.autocast(bfloat16))")
         return _exact_f32(variant, query, key, value, gate, beta, scale, initial_state, output_final_state,
                           cu_seqlens, out_dtype, state_shape)
     if not chunk and not (query.dtype == key.dtype == value.dtype == torch.bfloat16):
         # The recurrent kernel reads q, k, v as one element type: all bf16, or else all fp32 (an exact widening).
         query, key, value = (x if x.dtype == torch.float32 else x.float() for x in (query, key, value))
     if chunk:
-        # The chunk kernels take their MFMA operands in k's dtype, bf16 or f16, as the reference casts its dot
-        # operands to k.dtype; they read q, k, v with 16-byte rows.
-        query, value = query.to(key.dtype), value.to(key.dtype)
-        if grad and key.dtype != torch.bfloat16:
-            raise NotImplementedError(f"{name}: the chunk backward runs on bfloat16 q, k, v (got {key.dtype}); for "
-                                      "training pass bfloat16 inputs or run under torch.autocast(bfloat16)")
+        # The chunk kernels take their MFMA operands in one 16-bit type and read q, k, v with 16-byte rows.  As the
+        # reference casts its dot operands to k.dtype, that is k's dtype when k is bf16 or f16, else the 16-bit
+        # dtype among v and q (mixed fp32 / 16-bit inputs).  The backward kernels take bf16 operands, so a call
+        # that needs gradients runs on bf16 whatever the input dtypes; the casts are differentiable, so each
+        # input's gradient comes back in its own dtype.
+        operand = next((x.dtype for x in (key, value, query) if x.dtype in _OPERAND_DTYPES), torch.bfloat16)
+        if grad:
+            operand = torch.bfloat16
+        query, key, value = (x.to(operand) for x in (query, key, value))
         query, key, value = (_as_row_aligned(x) for x in (query, key, value))
         if gate is not None and variant != _lib.GDN:
             gate = _as_row_aligned(gate)
@@ -189,7 +189,9 @@ class _ChunkFunction(torch.autograd.Function):
         batch, heads, seq_len, key_dim = query.shape
         value_dim = value.shape[-1]
         device = query.device
-        out = torch.empty(batch, heads, seq_len, value_dim, device=device, dtype=out_dtype)
+        # the training forward writes bf16 or fp32 output; an f16 output is written in fp32 and rounded once
+        written = out_dtype if out_dtype in (torch.bfloat16, torch.float32) else torch.float32
+        out = torch.empty(batch, heads, seq_len, value_dim, device=device, dtype=written)
         final_state = torch.empty(batch, heads, key_dim, value_dim, device=device, dtype=torch.float32)
         args = _lib.make_args(variant, query, key, value, gate, beta, out, scale, initial_state, final_state)
         if os.environ.get("GDR_CHUNK_BWD_RECOMPUTE", "0") == "1":
@@ -201,7 +203,7 @@ class _ChunkFunction(torch.autograd.Function):
             _lib.chunk_forward_train(args, ctx.saved_ws, device)
         ctx.save_for_backward(query, key, value, gate, beta, initial_state)
         ctx.variant, ctx.scale = variant, scale
-        return out, final_state
+        return out.to(out_dtype), final_state
 
     @staticmethod
     def backward(ctx, d_out, d_final):

@@ -4,7 +4,8 @@ against autograd of the fp64 oracle on the same bf16-rounded inputs.
 Mirrors the reference's gradient check (src tests/test_kimi_delta_attention.py:46-53: loss = sum(out * grad_out)
 plus a final-state term, gradients for q, k, v, gate, beta and the initial state) over its grid of shapes and gate
 strengths (:107-114), for all four variants, plus the layer's transposed layout, partial requires_grad, an absent
-initial state and a longer sequence; fp32 values (which run the fp32 recurrence) are refused with a clear error.
+initial state, a longer sequence, fp32 values and f16 / fp32 inputs (run on bf16 operands), the reverse scan's
+32- and 64-column slices, and the benchmark's training shapes (a few heads against the oracle at the full length).
 The op's default training path (gdr_chunk_fwd_train keeping records, states and u; gdr_chunk_bwd_saved) is checked
 bit for bit against the recompute path (GDR_CHUNK_BWD_RECOMPUTE=1: plain forward, gdr_chunk_bwd).
 
@@ -144,12 +145,86 @@ def test_chunk_backward_long_sequence():
     _check("kda", inp, "kda T=1024")
 
 
-def test_chunk_backward_refuses_fp32_values():
-    """An fp32 value makes the op run the fp32 recurrence (no rounding to bf16), which has no backward."""
-    inp = workloads.make_inputs("kda", 1, 64, 2, 64, 64, seed=6, device="cuda")
-    v = inp.value.float().requires_grad_()
-    with pytest.raises(NotImplementedError, match="fp32"):
-        CHUNK_FNS["kda"](inp.query, inp.key, v, inp.gate, inp.beta)
+def test_chunk_backward_fp32_value():
+    """bf16 q, k with an fp32 value (the reference trains on such mixes, casting its dot operands to k.dtype): the
+    op runs on bf16 operands and returns the value's gradient in fp32; the output is fp32."""
+    inp = workloads.make_inputs("kda", 1, 1024, 2, 128, 128, seed=6, gate_scale=4.0, state_std=1.0)
+    inp.value = inp.value.float()
+    _check("kda", inp, "kda fp32 value T=1024")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["f16", "fp32"])
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_chunk_backward_f16_and_fp32_inputs(variant, dtype):
+    """f16 or fp32 q, k, v that need gradients run the chunk forward and backward on bf16 operands (the backward
+    kernels are bf16); each gradient comes back in its input's dtype.  The oracle differentiates the inputs' own
+    values in fp64, so the check includes the rounding of f16 / fp32 inputs to bf16."""
+    inp = workloads.make_inputs(variant, 2, 200, 2, 128, 128, seed=8, dtype=dtype, gate_scale=4.0, state_std=0.5)
+    _check(variant, inp, f"{variant} {dtype} inputs")
+
+
+def _slice_width(pairs, value_dim=128, cus=256):
+    """The value columns per reverse-scan workgroup that the library picks on a 256-CU MI355X (scan_slice)."""
+    return next((sl for sl in (64, 32) if pairs * (value_dim // sl) >= cus), 16)
+
+
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+@pytest.mark.parametrize("batch", [4, 8])
+def test_chunk_backward_wide_slices(variant, batch):
+    """64 and 128 (batch, head) pairs at H=16, d=128: the reverse scan runs 32- and 64-column slices (16-column
+    slices run in every smaller case above)."""
+    inp = workloads.make_inputs(variant, batch, 150, 16, 128, 128, seed=14, gate_scale=4.0, state_std=0.5)
+    _check(variant, inp, f"{variant} B{batch} H16: {_slice_width(batch * 16)}-column reverse-scan slices")
+
+
+def _check_heads(variant, inp, picks, label, seed=15):
+    """_check at a full benchmark shape: the GPU differentiates every head; the fp64 oracle differentiates only
+    the (batch, head) pairs in `picks` (heads are independent, and the loss is a sum over heads, so those pairs'
+    gradients are the same in both)."""
+    gen = torch.Generator().manual_seed(seed)
+    B, H, T, K = inp.query.shape
+    V = inp.value.shape[-1]
+    d_out = torch.randn(B, H, T, V, generator=gen).to(torch.bfloat16)
+    d_final = torch.randn(B, H, K, V, generator=gen)
+    gl = _leaves(inp, "cuda")
+    out, fin = _call(variant, gl, _gpu)
+    loss = (out.float() * d_out.cuda().float()).sum() + (fin * d_final.cuda()).sum()
+    g_need = [x for x in gl if x is not None]
+    g_grads = [g.cpu() for g in torch.autograd.grad(loss, g_need)]
+    del out, fin, loss
+    names = [n for n, x in zip(NAMES, gl) if x is not None]
+    for b, h in picks:
+        pick = lambda x: None if x is None else x.detach().cpu()[b:b + 1, h:h + 1].double().requires_grad_()
+        cl = [pick(x) for x in gl]
+        o_ref, s_ref = _call(variant, cl, _cpu)
+        loss_ref = (o_ref * d_out[b:b + 1, h:h + 1].double()).sum() + (s_ref * d_final[b:b + 1, h:h + 1].double()).sum()
+        c_grads = torch.autograd.grad(loss_ref, [x for x in cl if x is not None])
+        report = []
+        for name, a, r in zip(names, g_grads, c_grads):
+            a = a[b:b + 1, h:h + 1].double()
+            assert torch.isfinite(a).all(), name
+            err = ((a - r).abs().max() / r.abs().max().clamp_min(1e-30)).item()
+            report.append(f"{name} {err:.1e}")
+            assert err <= (GATE_TOL if name == "dgate" else GRAD_TOL), (name, b, h, err)
+        print(f"{label} (b={b}, h={h}): " + " ".join(report), flush=True)
+
+
+def test_chunk_backward_prefill_config():
+    """The prefill configuration the training leg of the benchmark times (B=4, T=4096, H=16, d=128, KDA, initial
+    state ~ N(0, 0.02)): three (batch, head) pairs against the oracle at the full T, covering the 0.69 GB backward
+    workspace's indexing, the 64-step reverse scan and the 32-column slices."""
+    print("kda backward B=4 T=4096 H=16 K=V=128", flush=True)
+    inp = workloads.make_inputs("kda", 4, 4096, 16, 128, 128, seed=16, state_std=0.02)
+    _check_heads("kda", inp, [(0, 0), (1, 9), (3, 15)], "kda backward prefill config")
+
+
+@pytest.mark.parametrize("variant", ["gdn", "gla", "deltanet"])
+def test_chunk_backward_variant_config(variant):
+    """The variant sweep shape (B=2, T=8192, H=16, d=128, no initial state): one head against the oracle at the
+    full T (128-step reverse scan, 16-column slices)."""
+    print(f"{variant} backward B=2 T=8192 H=16 K=V=128", flush=True)
+    inp = workloads.make_inputs(variant, 2, 8192, 16, 128, 128, seed=17)
+    _check_heads(variant, inp, [(1, 6)], f"{variant} backward variant config")
 
 
 def _grads(variant, inp, recompute, retain=False):

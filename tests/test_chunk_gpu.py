@@ -67,6 +67,13 @@ def test_chunk_matches_oracle(variant, case):
     _check(variant, inp, f"chunk {variant} {case}")
 
 
+@pytest.mark.parametrize("variant", oracle.VARIANTS)
+def test_chunk_wide_slices(variant):
+    """128 (batch, head) pairs at d=128: the state scan runs 64-column slices (two workgroups per head)."""
+    inp = workloads.make_inputs(variant, 8, 200, 16, 128, 128, seed=6, gate_scale=4.0, state_std=0.5, device="cuda")
+    _check(variant, inp, f"chunk {variant} B8 H16 (64-column slices)")
+
+
 @pytest.mark.parametrize("variant", ["kda", "gdn", "deltanet"])
 def test_chunk_correlated_keys(variant):
     """Consecutive keys nearly parallel (reference tests' `correlated` mode): the WY solve is ill-conditioned."""

@@ -7,8 +7,9 @@ when autocast is on (src/ops/utils.py:84-88).  Here:
     shows that the result is closer to the f16 inputs' exact answer than rounding those inputs to bf16 would allow;
   * fp32 q, k, v (the reference's CPU-runnable configuration is fp32) run the fp32 recurrence, every product and sum
     in fp32, held to 1e-4 against fp64, including packed sequences with an empty one;
-  * under torch.autocast(bfloat16) the layer's fp32 q, k and bf16 v are cast to bf16 first, exactly as the bf16 op;
-  * the backward takes bf16 only and says so for f16 and fp32 inputs.
+  * mixed fp32 / bf16 q, k, v run on bf16 operands, bit for bit the bf16 op on bf16-cast inputs;
+  * under torch.autocast(bfloat16) the layer's fp32 q, k and bf16 v are cast to bf16 first, exactly as the bf16 op.
+(The backward of f16 and fp32 inputs, which runs on bf16 operands, is checked in test_chunk_bwd_gpu.py.)
 """
 
 import pytest
@@ -106,9 +107,17 @@ def test_chunk_under_autocast_casts_to_bf16():
     assert out_error(out, ref_o) <= OUT_TOL and state_error(state, ref_s) <= STATE_TOL
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
-def test_chunk_backward_takes_bf16_only(dtype):
-    inp = workloads.make_inputs("kda", 1, 64, 2, 64, 64, seed=9, dtype=dtype, device="cuda")
-    q = inp.query.detach().clone().requires_grad_()
-    with pytest.raises(NotImplementedError, match="bfloat16"):
-        CHUNK_FNS["kda"](q, inp.key, inp.value, inp.gate, inp.beta)
+def test_chunk_mixed_fp32_and_bf16_inputs_run_on_bf16():
+    """Mixed dtypes without gradients (bf16 q, k with an fp32 value; fp32 q, k with a bf16 value) run the chunk
+    kernels on the 16-bit dtype, bit for bit the bf16 op on bf16-cast inputs, with the output in the value's dtype."""
+    inp = workloads.make_inputs("kda", 2, 200, 4, 128, 128, seed=9, state_std=0.02, device="cuda")
+    ref_o, ref_s = _run("kda", inp)
+    with torch.no_grad():
+        o1, s1 = CHUNK_FNS["kda"](inp.query, inp.key, inp.value.float(), inp.gate, inp.beta,
+                                  initial_state=inp.initial_state, output_final_state=True)
+        o2, s2 = CHUNK_FNS["kda"](inp.query.float(), inp.key.float(), inp.value, inp.gate, inp.beta,
+                                  initial_state=inp.initial_state, output_final_state=True)
+    torch.cuda.synchronize()
+    assert o1.dtype == torch.float32 and o2.dtype == torch.bfloat16
+    assert torch.equal(o2, ref_o) and torch.equal(s2, ref_s) and torch.equal(s1, ref_s)
+    assert torch.equal(o1.bfloat16(), ref_o)
