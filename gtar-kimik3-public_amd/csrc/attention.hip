@@ -20,6 +20,7 @@
 // P V (uniform branches around VALU work; no MFMA sits under a data-dependent branch).  K tiles run one ahead of V
 // tiles, so each tile's exponentials interleave with the next tile's score MFMAs in one basic block.
 #include "chunk_common.h"
+#include "varlen_index.h"
 #include "gdr_internal.h"
 
 namespace gdr {
@@ -69,8 +70,6 @@ __device__ __forceinline__ V8 cat(V4 lo, V4 hi) {
   return V8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// First query-block slot of packed sequence n: floor(bos / kBM) + n (slots of consecutive sequences never overlap).
-__device__ __forceinline__ int attn_slot_base(const int32_t* cu, int n) { return cu[n] / kBM + n; }
 
 template <int D, typename T>
 __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gdr_attention_args a, int nqb) {
@@ -91,17 +90,12 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
   const int H = a.heads;
   const int h = blockIdx.x % H, slot = blockIdx.x / H;
   int n, qb, bos = 0, len = a.seq_len;
-  if (a.cu_seqlens) {
-    int lo = 0, hi = a.n_seqs - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (attn_slot_base(a.cu_seqlens, mid) <= slot) lo = mid; else hi = mid - 1;
-    }
-    n = lo;
-    bos = a.cu_seqlens[n];
-    len = a.cu_seqlens[n + 1] - bos;
+  if (a.cu_seqlens) {  // query-block slots: floor(bos / kBM) + n is the first of sequence n (clamped offsets)
+    n = packed_slot_seq(a.cu_seqlens, a.n_seqs, a.seq_len, kBM, slot);
+    bos = packed_begin(a.cu_seqlens, n, a.seq_len);
+    len = packed_end(a.cu_seqlens, n, a.seq_len) - bos;
     const int nb = (len + kBM - 1) / kBM;
-    const int r = slot - attn_slot_base(a.cu_seqlens, n);
+    const int r = slot - packed_slot_base(a.cu_seqlens, n, a.seq_len, kBM);
     if (r < 0 || r >= nb) return;  // gap slot: uniform over the workgroup, before any barrier
     qb = nb - 1 - r;
   } else {

@@ -40,6 +40,7 @@
 //     is a blocked forward substitution on v_mfma_f32_16x16x16_bf16 from registers; the state update reads
 //     (K e^{b_end - b})^T with the gfx950 transposing LDS read (ds_read_b64_tr_b16) from the row-major tile.
 #include "chunk_common.h"
+#include "varlen_index.h"
 #include "gdr_internal.h"
 
 namespace gdr {
@@ -545,10 +546,8 @@ __global__ __launch_bounds__(512, 1) void chunk_fwd_kernel(const gdr_args a, int
   const int n = bh / H, h = bh % H;
   int bos = 0, len = a.seq_len, bidx = n;
   if (a.cu_seqlens) {
-    const int lo = min(max(a.cu_seqlens[n], 0), a.seq_len);
-    const int hi = min(max(a.cu_seqlens[n + 1], lo), a.seq_len);
-    bos = lo;
-    len = hi - lo;
+    bos = packed_begin(a.cu_seqlens, n, a.seq_len);
+    len = packed_end(a.cu_seqlens, n, a.seq_len) - bos;
     bidx = 0;
   }
   ChunkCtx x;

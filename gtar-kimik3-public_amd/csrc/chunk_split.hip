@@ -239,15 +239,10 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
   const int h = blockIdx.x % H;
   int slot = blockIdx.x / H, n, c, bos = 0, len = a.seq_len;
   if (a.cu_seqlens) {
-    int lo = 0, hi = a.n_seqs - 1;  // largest n with base(n) <= slot
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (varlen_base(a.cu_seqlens, mid) <= slot) lo = mid; else hi = mid - 1;
-    }
-    n = lo;
-    bos = a.cu_seqlens[n];
-    len = a.cu_seqlens[n + 1] - bos;
-    c = slot - varlen_base(a.cu_seqlens, n);
+    n = packed_slot_seq(a.cu_seqlens, a.n_seqs, a.seq_len, kChunk, slot);
+    bos = packed_begin(a.cu_seqlens, n, a.seq_len);
+    len = packed_end(a.cu_seqlens, n, a.seq_len) - bos;
+    c = slot - varlen_base(a.cu_seqlens, n, a.seq_len);
     if (c < 0 || c * kChunk >= len) return;  // gap slot: uniform over the workgroup, before any barrier
   } else {
     // Launch order is chunk-major from the last chunk down: the records written last are the first chunks, which
@@ -884,9 +879,9 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::threads(kMode)), 1) void chunk_
   const int n = bh / H, h = bh % H;
   int bos = 0, len = a.seq_len, base = n * nc, bidx = n;
   if (a.cu_seqlens) {
-    bos = a.cu_seqlens[n];
-    len = a.cu_seqlens[n + 1] - bos;
-    base = varlen_base(a.cu_seqlens, n);
+    bos = packed_begin(a.cu_seqlens, n, a.seq_len);
+    len = packed_end(a.cu_seqlens, n, a.seq_len) - bos;
+    base = varlen_base(a.cu_seqlens, n, a.seq_len);
     bidx = 0;
   }
   const int nchunks = (len + kChunk - 1) / kChunk;

@@ -9,6 +9,7 @@
 // its channels with W 16-byte loads, accumulates in fp32 and stores each output once.  HBM-bound: x read about once
 // (neighbouring threads' overlapping rows hit L2), out written once.
 #include "gdr_common.h"
+#include "varlen_index.h"
 #include "gdr_internal.h"
 
 namespace gdr {
@@ -62,8 +63,8 @@ __global__ __launch_bounds__(256) void short_conv_kernel(const gdr_conv_args a, 
   int n = b, bos = 0, end = a.seq_len;
   if (a.cu_seqlens) {
     n = seq_of(a.cu_seqlens, a.n_seqs, t0);
-    bos = a.cu_seqlens[n];
-    end = a.cu_seqlens[n + 1];
+    bos = packed_begin(a.cu_seqlens, n, a.seq_len);
+    end = packed_end(a.cu_seqlens, n, a.seq_len);
   }
 #pragma unroll
   for (int k = 0; k < kConvTok; ++k) {
@@ -71,10 +72,11 @@ __global__ __launch_bounds__(256) void short_conv_kernel(const gdr_conv_args a, 
     if (t >= a.seq_len) break;
     while (t >= end && n + 1 < a.n_seqs) {  // the next packed sequence starts inside this thread's tokens
       ++n;
-      bos = end;
-      end = a.cu_seqlens[n + 1];
+      bos = packed_begin(a.cu_seqlens, n, a.seq_len);
+      end = packed_end(a.cu_seqlens, n, a.seq_len);
     }
-    if (t >= end) break;  // past cu_seqlens[n_seqs] (a caller that breaks the offsets contract): nothing to do
+    // past the last sequence's end, or before this sequence's start (offsets that break the contract): nothing to do
+    if (t >= end || t < bos) break;
     const size_t state_row = size_t(n) * C;  // [N, C, W - 1]
     float acc[VEC];
 #pragma unroll

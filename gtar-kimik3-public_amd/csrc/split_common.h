@@ -3,6 +3,7 @@
 #pragma once
 
 #include "chunk_common.h"
+#include "varlen_index.h"
 
 namespace gdr {
 namespace chunk {
@@ -44,10 +45,8 @@ __device__ __forceinline__ void store4(float* dst, floatx4 v) {
   *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
-// First workspace slot of packed sequence n: floor(bos / 64) + n.  Slots of consecutive sequences never
-// overlap (floor(a + b) >= floor(a) + floor(b) and floor(len / 64) + 1 >= ceil(len / 64)) and every slot is below
-// ceil(T / 64) + n_seqs.
-__device__ __forceinline__ int varlen_base(const int32_t* cu, int n) { return cu[n] / kChunk + n; }
+// First workspace slot of packed sequence n (clamped offsets, one slot per chunk): floor(bos / 64) + n.
+__device__ __forceinline__ int varlen_base(const int32_t* cu, int n, int T) { return packed_slot_base(cu, n, T, kChunk); }
 
 }  // namespace chunk
 }  // namespace gdr
