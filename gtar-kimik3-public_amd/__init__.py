@@ -9,6 +9,7 @@ For the hybrid stack around the op, `flash_attention` (causal grouped-query atte
 and `short_convolution` (src/layers/short_convolution.py) take packed sequences through `cu_seqlens`.
 """
 
+from ._common import set_chunk_backward_workspace
 from .attention import flash_attention
 from .cache import RecurrentCache
 from .conv import short_convolution
@@ -35,6 +36,7 @@ __all__ = [
     "recurrent_gated_deltanet",
     "recurrent_gated_linear_attention",
     "recurrent_kimi_delta_attention",
+    "set_chunk_backward_workspace",
     "short_convolution",
     "VerifiedBlock",
     "verify_deltanet",

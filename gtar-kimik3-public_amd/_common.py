@@ -16,8 +16,8 @@ The chunk ops are differentiable like the reference's torch.autograd.Function cl
 `_ChunkFunction`, returning gradients for q, k, v, gate, beta and the initial state (none for `scale`).  Its
 forward is gdr_chunk_fwd_train, which also keeps the forward records, the per-chunk states and u in the backward
 workspace, and its backward is gdr_chunk_bwd_saved on that workspace.  The reference's backward recomputes the
-states instead (:566-571); with GDR_CHUNK_BWD_RECOMPUTE=1 in the environment this module does the same (plain
-forward, gdr_chunk_bwd), holding less memory between forward and backward.
+states instead (:566-571); `set_chunk_backward_workspace(False)` (or GDR_CHUNK_BWD_RECOMPUTE=1 in the environment)
+makes this module do the same (plain forward, gdr_chunk_bwd), holding less memory between forward and backward.
 Differences, all deliberate: CPU tensors raise (the reference's CPU token loop is this repository's test oracle,
 not a product path); gradients through the recurrent ops raise (the reference's recurrent ops have none either)
 and so do gradients of packed varlen calls; packed variable-length input is accepted through `cu_seqlens` (the
@@ -34,6 +34,31 @@ from . import _lib
 
 _VARIANT_NAMES = {_lib.KDA: "kimi delta attention", _lib.GDN: "gated deltanet", _lib.GLA: "gated linear attention",
                   _lib.DELTANET: "deltanet"}
+
+
+_KEEP_WORKSPACE = None  # None: decided per call by the GDR_CHUNK_BWD_RECOMPUTE environment variable
+
+
+def set_chunk_backward_workspace(keep: bool | None) -> None:
+    """Choose what the chunk ops' training forward keeps for the backward.
+
+    keep=True: the forward (gdr_chunk_fwd_train) fills the backward workspace -- the per-chunk records, the bf16
+    state entering every chunk, the bf16 u, and room for the backward's state gradients -- and keeps it until the
+    backward runs, which then skips recomputing them.  That is gdr_chunk_bwd_workspace_bytes per call, 0.69 GB at
+    B=4, T=4096, H=16, K=V=128, held per layer from forward to backward.
+    keep=False: the forward keeps only its inputs and the backward recomputes the records and states (a prep launch
+    and a state scan, about 0.29 ms at that shape), as the reference's backward does
+    (src/ops/kimi_delta_attention.py:566-571).  keep=None (the default) reads GDR_CHUNK_BWD_RECOMPUTE on each call:
+    "1" recomputes, anything else keeps.
+    """
+    global _KEEP_WORKSPACE
+    _KEEP_WORKSPACE = keep
+
+
+def _keep_workspace() -> bool:
+    if _KEEP_WORKSPACE is not None:
+        return _KEEP_WORKSPACE
+    return os.environ.get("GDR_CHUNK_BWD_RECOMPUTE", "0") != "1"
 
 
 def _autocast(*tensors):
@@ -194,7 +219,7 @@ class _ChunkFunction(torch.autograd.Function):
         out = torch.empty(batch, heads, seq_len, value_dim, device=device, dtype=written)
         final_state = torch.empty(batch, heads, key_dim, value_dim, device=device, dtype=torch.float32)
         args = _lib.make_args(variant, query, key, value, gate, beta, out, scale, initial_state, final_state)
-        if os.environ.get("GDR_CHUNK_BWD_RECOMPUTE", "0") == "1":
+        if not _keep_workspace():
             ctx.saved_ws = None
             workspace = _lib.chunk_workspace(args, device)  # noqa: F841 (alive until enqueued)
             _lib.launch("gdr_chunk_fwd", args, device)

@@ -87,9 +87,11 @@ typedef struct gdr_args {
  *   ChunkGatedLinearAttention   src/ops/gated_linear_attention.py:362-384
  *   ChunkDeltaNet               src/ops/deltanet.py:326-347
  * (pad_sequence + chunk_cumsum + kernel matrices + WY representation + state scan + output, six launches and
- * a [B,H,NC+1,K,V] States buffer in the reference) with one fused launch.  q, k, v must be bf16 (the MFMA
- * operand type; the Python layer casts); out may be bf16, f16 or f32.
- * Supports K in {64, 128}, V a multiple of 64, any T >= 1, and packed varlen input through cu_seqlens. */
+ * a [B,H,NC+1,K,V] States buffer in the reference).  With a workspace it is two launches on `stream`: a
+ * chunk-parallel preparation kernel that writes one record per (chunk, head) into the workspace, then the state
+ * scan that reads them; with workspace NULL it is one slower launch that needs no scratch.  q, k, v must be all
+ * bf16 or all f16 (the MFMA operand type; the Python layer casts); out may be bf16, f16 or f32.
+ * Supports K in {64, 128}, V a multiple of 64, any T >= 0, and packed varlen input through cu_seqlens. */
 int gdr_chunk_fwd(const gdr_args* args, hipStream_t stream);
 
 /* Fused layer prologue for gdr_chunk_fwd_fused: the per-token work the reference's KDA layer does in PyTorch before
@@ -141,9 +143,8 @@ int64_t gdr_chunk_workspace_bytes(const gdr_args* args);
 
 /* gdr_chunk_fwd without a workspace and without any allocation: the two-launch path runs on a scratch array of
  * GDR_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on, from the first call on that GPU until the
- * process ends.  No counterpart in the reference (whose op allocates its intermediates per call,
- * src/ops/kimi_delta_attention.py:540-553): it is for callers that cannot allocate device memory -- code under
- * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.  Calls no hipMalloc, hipFree or
+ * process ends.  It has no counterpart in the reference: it is for callers that cannot allocate device memory --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.  Calls no hipMalloc, hipFree or
  * allocating library routine.  args->workspace must be NULL; a call whose gdr_chunk_workspace_bytes exceeds
  * GDR_NOALLOC_SCRATCH_BYTES (e.g. more than 1,885 chunk-head records at K = V = 128: B = 1, T = 4096, H = 16 fits)
  * returns GDR_ERR_UNSUPPORTED.  Nothing in the scratch needs clearing: the preparation launch writes every record

@@ -7,18 +7,16 @@ strengths (:107-114), for all four variants, plus the layer's transposed layout,
 initial state, a longer sequence, fp32 values and f16 / fp32 inputs (run on bf16 operands), the reverse scan's
 32- and 64-column slices, and the benchmark's training shapes (a few heads against the oracle at the full length).
 The op's default training path (gdr_chunk_fwd_train keeping records, states and u; gdr_chunk_bwd_saved) is checked
-bit for bit against the recompute path (GDR_CHUNK_BWD_RECOMPUTE=1: plain forward, gdr_chunk_bwd).
+bit for bit against the recompute path (set_chunk_backward_workspace(False): plain forward, gdr_chunk_bwd).
 
 Tolerance: max|d - d_ref| <= 2e-2 * max|d_ref| for dq, dk, dv, dbeta and d(initial state); 3e-2 for the gate
 gradient, a reverse cumulative sum over each chunk of terms that each carry bf16 operand rounding.
 """
 
-import os
-
 import pytest
 import torch
 
-from _helpers import CHUNK_FNS, oracle, workloads
+from _helpers import CHUNK_FNS, gdr, oracle, workloads
 
 pytestmark = pytest.mark.gpu
 
@@ -231,8 +229,7 @@ def _grads(variant, inp, recompute, retain=False):
     gen = torch.Generator().manual_seed(11)
     d_out = torch.randn(inp.value.shape, generator=gen).to(inp.value.dtype).cuda()
     d_final = torch.randn(inp.initial_state.shape, generator=gen).cuda()
-    old = os.environ.get("GDR_CHUNK_BWD_RECOMPUTE")
-    os.environ["GDR_CHUNK_BWD_RECOMPUTE"] = "1" if recompute else "0"
+    gdr.set_chunk_backward_workspace(not recompute)
     try:
         gl = _leaves(inp, "cuda")
         out, fin = _call(variant, gl, _gpu)
@@ -240,10 +237,7 @@ def _grads(variant, inp, recompute, retain=False):
         grads = torch.autograd.grad([out, fin], need, [d_out, d_final], retain_graph=retain)
         again = torch.autograd.grad([out, fin], need, [d_out, d_final]) if retain else None
     finally:
-        if old is None:
-            del os.environ["GDR_CHUNK_BWD_RECOMPUTE"]
-        else:
-            os.environ["GDR_CHUNK_BWD_RECOMPUTE"] = old
+        gdr.set_chunk_backward_workspace(None)
     torch.cuda.synchronize()
     return out.detach(), fin.detach(), grads, again
 

@@ -74,6 +74,42 @@ def test_noalloc_varlen_and_fp32_out_match_chunk_fwd():
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
 
 
+@pytest.mark.gpu
+def test_noalloc_under_graph_capture_matches_chunk_fwd():
+    """gdr_chunk_fwd_noalloc captured in a torch.cuda.CUDAGraph (the callers it is for include code under graph
+    capture): each replay, with eager work and a synchronisation between replays, equals eager gdr_chunk_fwd bit for
+    bit.  The captured call allocates nothing, so its output buffers come from the graph's memory pool."""
+    dev = torch.device("cuda")
+    inp = workloads.make_inputs("kda", 1, 1000, 8, 128, 128, seed=5, state_std=0.02, device=dev)
+    ref_o, ref_s = _fwd("gdr_chunk_fwd", lib.KDA, inp)
+    so = lib.load_library()
+
+    def launch(stream):
+        q, k, v = inp.query, inp.key, inp.value
+        out = torch.empty(v.shape, device=dev, dtype=torch.bfloat16)
+        ht = torch.empty_like(inp.initial_state)
+        args = lib.make_args(lib.KDA, q, k, v, inp.gate, inp.beta, out, 128 ** -0.5, inp.initial_state, ht)
+        rc = so.gdr_chunk_fwd_noalloc(ctypes.byref(args), ctypes.c_void_p(stream.cuda_stream))
+        assert rc == 0, so.gdr_last_error().decode()
+        return out, ht
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch(side)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap_o, cap_s = launch(torch.cuda.current_stream())
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(cap_o, ref_o) and torch.equal(cap_s, ref_s), f"replay {i}"
+        _fwd("gdr_chunk_fwd", lib.KDA, inp)  # eager work between replays
+        torch.cuda.synchronize()
+
+
 def _host_args(B, T, H, K=128, V=128):
     """A gdr_args with placeholder (never dereferenced) pointers: the checks below fail before any device work."""
     args = lib.GdrArgs()
