@@ -44,7 +44,9 @@ chunkwise == recurrence at several chunk sizes, state passing between segments, 
 varlen == per-sequence runs; `layer_prologue` against torch.nn.functional's normalize / softplus / sigmoid and
 nn.Linear, `causal_attention` against F.scaled_dot_product_attention (is_causal, enable_gqa) and
 `short_convolution` against nn.Conv1d / F.conv1d as the reference module calls them (library routines), each also
-per packed sequence; `rms_norm` against F.rms_norm.  `hybrid_stack` is a composition of pinned pieces.  No function is left "parity unpinned".
+per packed sequence; `rms_norm` against F.rms_norm; `hybrid_stack` against the reference's own KimiK3Block
+classes, run in fp32 on CPU by tests/golden/make_stack_golden.py (the fixture tests/golden/stack_reference.npz holds
+each block's output and each KDA layer's final state per packed sequence).  No function is left "parity unpinned".
 
 Layouts follow the reference: q, k [B, H, T, K]; v [B, H, T, V]; gate [B, H, T, K] (KDA, GLA) or [B, H, T]
 (GDN); beta [B, H, T]; state [B, H, K, V].

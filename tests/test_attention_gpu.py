@@ -88,7 +88,8 @@ def test_attention_full_packed_shape_equals_each_sequence_alone():
     """The stack's packed configuration at its stated shape (32 sequences with lengths ~U[256, 4096], 16 query /
     8 key-value heads, head dim 128, bf16): the packed call equals each sequence run on its own bit for bit (the
     tiles start at each sequence's first token either way), a property that holds at any size, so no fp64 oracle
-    has to run the full shape; the oracle bar is checked on the shortest sequence."""
+    has to run the full shape; the oracle bar is checked on the shortest sequence (every head) and on the longest
+    one (two query heads of different key-value heads)."""
     workloads = importlib.import_module("gtar-kimik3-public_amd.workloads")
     lengths = workloads.varlen_lengths(32, 256, 4096, seed=0)
     cu = torch.tensor([0] + torch.tensor(lengths).cumsum(0).tolist(), dtype=torch.int32)
@@ -111,6 +112,17 @@ def test_attention_full_packed_shape_equals_each_sequence_alone():
     base = (sdpa.double() - exact).abs().max().item()
     print(f"  sequence {i} ({e - s} tokens): kernel {err:.2e}  sdpa {base:.2e}")
     assert err <= 2 * base + 1e-4
+    i = max(range(len(lengths)), key=lambda j: lengths[j])
+    s, e = int(cu[i]), int(cu[i + 1])
+    for h in (0, 11):  # query head h reads key-value head h // 2
+        qs = q[:, h:h + 1, s:e].cpu()
+        ks, vs = (x[:, h // 2:h // 2 + 1, s:e].cpu() for x in (k, v))
+        exact = oracle.causal_attention(qs, ks, vs)
+        sdpa = F.scaled_dot_product_attention(qs, ks, vs, is_causal=True)
+        err = (out[:, h:h + 1, s:e].cpu().double() - exact).abs().max().item()
+        base = (sdpa.double() - exact).abs().max().item()
+        print(f"  sequence {i} ({e - s} tokens), head {h}: kernel {err:.2e}  sdpa {base:.2e}")
+        assert err <= 2 * base + 1e-4
 
 
 def test_attention_scale_and_autocast():
