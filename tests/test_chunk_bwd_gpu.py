@@ -175,7 +175,7 @@ def test_chunk_backward_wide_slices(variant, batch):
     _check(variant, inp, f"{variant} B{batch} H16: {_slice_width(batch * 16)}-column reverse-scan slices")
 
 
-def _check_heads(variant, inp, picks, label, seed=15):
+def _check_heads(variant, inp, picks, label, seed=15, gate_tol=GATE_TOL):
     """_check at a full benchmark shape: the GPU differentiates every head; the fp64 oracle differentiates only
     the (batch, head) pairs in `picks` (heads are independent, and the loss is a sum over heads, so those pairs'
     gradients are the same in both)."""
@@ -203,7 +203,7 @@ def _check_heads(variant, inp, picks, label, seed=15):
             assert torch.isfinite(a).all(), name
             err = ((a - r).abs().max() / r.abs().max().clamp_min(1e-30)).item()
             report.append(f"{name} {err:.1e}")
-            assert err <= (GATE_TOL if name == "dgate" else GRAD_TOL), (name, b, h, err)
+            assert err <= (gate_tol if name == "dgate" else GRAD_TOL), (name, b, h, err)
         print(f"{label} (b={b}, h={h}): " + " ".join(report), flush=True)
 
 
@@ -214,6 +214,17 @@ def test_chunk_backward_prefill_config():
     print("kda backward B=4 T=4096 H=16 K=V=128", flush=True)
     inp = workloads.make_inputs("kda", 4, 4096, 16, 128, 128, seed=16, state_std=0.02)
     _check_heads("kda", inp, [(0, 0), (1, 9), (3, 15)], "kda backward prefill config")
+
+
+@pytest.mark.parametrize("variant", ["kda", "gdn"])
+def test_chunk_backward_gate_gradient_long_sequence_large_state(variant):
+    """The gate gradient's boundary term rowsum(S (x) dS') is formed from the bf16 states and state gradients the
+    reverse scan stores (the reference's _chunk_gate_gradient uses fp32 ones, kimi_delta_attention.py:484-490).
+    Over a long sequence (T=4096) with a large state (initial state ~ N(0, 1), slow decay), the gate gradient stays
+    within 1e-2 of the fp64 oracle, a third of the 3e-2 bound the other cases use."""
+    print(f"{variant} backward B=1 T=4096 H=2 K=V=128, state ~ N(0, 1)", flush=True)
+    inp = workloads.make_inputs(variant, 1, 4096, 2, 128, 128, seed=18, gate_scale=16.0, state_std=1.0)
+    _check_heads(variant, inp, [(0, 0), (0, 1)], f"{variant} long sequence, large state", gate_tol=1e-2)
 
 
 @pytest.mark.parametrize("variant", ["gdn", "gla", "deltanet"])
