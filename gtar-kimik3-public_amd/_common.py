@@ -136,16 +136,20 @@ def run(variant: int, chunk: bool, query, key, value, gate, beta, scale, initial
             raise ValueError(f"{name}: initial_state must have shape {state_shape}, got {tuple(initial_state.shape)}")
         initial_state = initial_state.float().contiguous()
 
-    if chunk and not grad and all(x.dtype == torch.float32 for x in (query, key, value)):
-        # The reference's chunk kernels take their dot operands in the input dtype (.to(k.dtype),
-        # kimi_delta_attention.py:99-100, :130, :135): fp32 inputs get fp32 products.  The chunk kernels multiply
-        # 16-bit operands, so fp32 input runs the recurrence instead (every product and sum in fp32).
-        return _exact_f32(variant, query, key, value, gate, beta, scale, initial_state, output_final_state,
-                          cu_seqlens, out_dtype, state_shape)
-    if not chunk and not (query.dtype == key.dtype == value.dtype == torch.bfloat16):
+    # The sequential path of the chunk op (libgdr's gdr_chunk_fwd runs the recurrent kernel over every token, the
+    # state, every product and every sum in fp32): fp32 q, k, v when no gradient is needed -- the reference's chunk
+    # kernels take their dot operands in the input dtype (.to(k.dtype), kimi_delta_attention.py:99-100, :130, :135),
+    # so fp32 inputs get fp32 products, and the chunk kernels multiply 16-bit operands -- and key dims the chunk
+    # kernels are not built for (they take 64 and 128; the reference's take any multiple of 64).
+    sequential = chunk and (key_dim not in (64, 128) or
+                            (not grad and all(x.dtype == torch.float32 for x in (query, key, value))))
+    if sequential and grad:
+        raise NotImplementedError(f"{name}: key dim {key_dim} runs the recurrent kernel, which has no backward (the "
+                                  "chunk backward takes key dims 64 and 128)")
+    if (sequential or not chunk) and not (query.dtype == key.dtype == value.dtype == torch.bfloat16):
         # The recurrent kernel reads q, k, v as one element type: all bf16, or else all fp32 (an exact widening).
         query, key, value = (x if x.dtype == torch.float32 else x.float() for x in (query, key, value))
-    if chunk:
+    if chunk and not sequential:
         # The chunk kernels take their MFMA operands in one 16-bit type and read q, k, v with 16-byte rows.  As the
         # reference casts its dot operands to k.dtype, that is k's dtype when k is bf16 or f16, else the 16-bit
         # dtype among v and q (mixed fp32 / 16-bit inputs).  The backward kernels take bf16 operands, so a call
@@ -167,40 +171,12 @@ def run(variant: int, chunk: bool, query, key, value, gate, beta, scale, initial
     out = torch.empty(batch, heads, seq_len, value_dim, device=device, dtype=out_dtype)
     final_state = torch.empty(state_shape, device=device, dtype=torch.float32) if output_final_state else None
     args = _lib.make_args(variant, query, key, value, gate, beta, out, scale, initial_state, final_state, cu_seqlens)
-    workspace = _lib.chunk_workspace(args, device) if chunk else None  # noqa: F841 (alive until enqueued)
+    workspace = _lib.chunk_workspace(args, device) if chunk and not sequential else None  # noqa: F841 (alive until enqueued)
     _lib.launch("gdr_chunk_fwd" if chunk else "gdr_recurrent_fwd", args, device)
     return (out, final_state) if output_final_state else out
 
 
 _OPERAND_DTYPES = (torch.bfloat16, torch.float16)
-
-
-def _exact_f32(variant, query, key, value, gate, beta, scale, initial_state, output_final_state, cu_seqlens,
-               out_dtype, state_shape):
-    """The chunk op on fp32 q, k, v: libgdr's recurrent kernel over all T tokens, which keeps the state, every
-    product and every sum in fp32 (the chunkwise form is an exact regrouping of this recurrence).  Packed sequences
-    run one recurrent call each."""
-    device = query.device
-    query, key, value = (x.float() for x in (query, key, value))
-    out = torch.empty(*query.shape[:3], value.shape[-1], device=device, dtype=out_dtype)
-    final_state = torch.empty(state_shape, device=device, dtype=torch.float32) if output_final_state else None
-    if cu_seqlens is None:
-        spans = [(slice(None), None)]
-    else:
-        bounds = cu_seqlens.tolist()
-        spans = [(slice(bounds[i], bounds[i + 1]), i) for i in range(len(bounds) - 1)]
-    for span, n in spans:
-        pick = (lambda x: x) if n is None else (lambda x: x[n:n + 1])
-        cut = lambda x: None if x is None else x[:, :, span]
-        h0 = None if initial_state is None else pick(initial_state)
-        ht = None if final_state is None else pick(final_state)
-        if n is not None and bounds[n + 1] == bounds[n]:  # an empty sequence keeps its state
-            if ht is not None:
-                ht.copy_(h0 if h0 is not None else torch.zeros_like(ht))
-            continue
-        args = _lib.make_args(variant, cut(query), cut(key), cut(value), cut(gate), cut(beta), cut(out), scale, h0, ht)
-        _lib.launch("gdr_recurrent_fwd", args, device)
-    return (out, final_state) if output_final_state else out
 
 
 class _ChunkFunction(torch.autograd.Function):

@@ -42,6 +42,25 @@ int check_view(const gdr_tensor& t, const char* name, bool required, bool f32_on
   return GDR_OK;
 }
 
+// Whether a chunk-mode call runs the sequential path -- the recurrent kernel over every token of each sequence, the
+// state, every product and every sum in fp32 -- instead of the chunk kernels: q, k, v all fp32 (the reference's
+// kernels take fp32 dot operands for fp32 inputs, src/ops/kimi_delta_attention.py:99-100, :130), or a key dim the
+// chunk kernels are not built for (they take 64 and 128; the reference's take any multiple of 64).
+bool chunk_sequential(const gdr_args* a) {
+  const bool f32 = a->q.dtype == GDR_F32 && a->k.dtype == GDR_F32 && a->v.dtype == GDR_F32;
+  return f32 || (a->key_dim != 64 && a->key_dim != 128);
+}
+
+// The chunk backward's shapes: the chunk kernels' key dims (64, 128) and value dims (multiples of 64).
+int check_bwd_shape(const gdr_args* a) {
+  if (a->key_dim != 64 && a->key_dim != 128)
+    return fail(GDR_ERR_UNSUPPORTED, "the chunk backward takes key dims 64 and 128 (got %d)", a->key_dim);
+  if (a->value_dim % 64)
+    return fail(GDR_ERR_UNSUPPORTED, "the chunk backward takes value dims that are multiples of 64 (got %d)",
+                a->value_dim);
+  return GDR_OK;
+}
+
 // Sizes, variant, head dims and varlen fields: everything that shapes the work, no pointer dereferenced.
 int check_shape(const gdr_args* a, bool chunk) {
   if (!a) return fail(GDR_ERR_INVALID, "args is NULL");
@@ -51,9 +70,12 @@ int check_shape(const gdr_args* a, bool chunk) {
     return fail(GDR_ERR_INVALID, "unknown variant %d", a->variant);
   if (a->batch < 1 || a->heads < 1 || a->seq_len < 0)
     return fail(GDR_ERR_INVALID, "bad sizes B=%d H=%d T=%d", a->batch, a->heads, a->seq_len);
-  if (a->key_dim != 64 && a->key_dim != 128)
-    return fail(GDR_ERR_UNSUPPORTED, "key dim %d not supported (64 or 128)", a->key_dim);
-  const int vmul = chunk ? 64 : 32;
+  // The recurrent kernel takes key dims 32, 64, 128, 192 and 256 (the powers of two the reference's recurrent kernel
+  // takes up to 256, and the multiples of 64 its chunk kernels take up to 256); the chunk kernels take 64 and 128.
+  const int K = a->key_dim;
+  if (K != 32 && K != 64 && K != 128 && K != 192 && K != 256)
+    return fail(GDR_ERR_UNSUPPORTED, "key dim %d not supported (32, 64, 128, 192 or 256)", K);
+  const int vmul = chunk && !chunk_sequential(a) ? 64 : 32;
   if (a->value_dim < vmul || a->value_dim % vmul != 0 || a->value_dim > 1024)
     return fail(GDR_ERR_UNSUPPORTED, "value dim %d not supported (a multiple of %d up to 1024)", a->value_dim,
                 vmul);
@@ -158,9 +180,26 @@ hipError_t scratch_on_device(int device, void** out) {
   return hipSuccess;
 }
 
+// The chunk op on the sequential path (chunk_sequential): q, k, v of one dtype, bf16 or f32, read by the recurrent
+// kernel one token at a time, packed sequences included; no workspace is used.
+int chunk_fwd_sequential(const gdr_args* a, const gdr_prologue* pro, hipStream_t stream) {
+  if (pro) return fail(GDR_ERR_UNSUPPORTED, "the fused prologue runs on the chunk kernels: key dims 64 and 128, bf16 q, "
+                       "k, v (got key dim %d, dtype codes %d, %d, %d)", a->key_dim, a->q.dtype, a->k.dtype, a->v.dtype);
+  int rc = check_common(a, true);
+  if (rc) return rc;
+  if (a->q.dtype != a->k.dtype || a->q.dtype != a->v.dtype || a->q.dtype == GDR_F16)
+    return fail(GDR_ERR_UNSUPPORTED, "key dim %d runs the recurrent kernel, which reads q, k, v of one dtype, bf16 or f32 "
+                "(got dtype codes %d, %d, %d)", a->key_dim, a->q.dtype, a->k.dtype, a->v.dtype);
+  hipError_t e = gdr::launch_recurrent(*a, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "recurrent launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
 int chunk_fwd(const gdr_args* a, const gdr_prologue* pro, hipStream_t stream) {
   int rc = check_shape(a, true);
   if (rc) return rc;
+  if (chunk_sequential(a)) return chunk_fwd_sequential(a, pro, stream);
   if (pro && (rc = check_prologue(a, pro))) return rc;
   const bool lowrank = pro && (pro->flags & GDR_PRO_GATE_LOWRANK);
   if ((rc = check_common(a, true, true, !lowrank))) return rc;
@@ -208,6 +247,7 @@ int check_bwd(const gdr_args* a, const gdr_grads* g, void* workspace, int64_t wo
   if (rc) return rc;
   if (!g) return fail(GDR_ERR_INVALID, "grads is NULL");
   if (a->cu_seqlens) return fail(GDR_ERR_UNSUPPORTED, "the chunk backward does not take packed varlen input");
+  if ((rc = check_bwd_shape(a))) return rc;
   if (a->q.dtype != GDR_BF16 || a->k.dtype != GDR_BF16 || a->v.dtype != GDR_BF16)
     return fail(GDR_ERR_UNSUPPORTED, "the chunk backward reads bf16 q, k, v (got dtype codes %d, %d, %d)", a->q.dtype,
                 a->k.dtype, a->v.dtype);
@@ -442,7 +482,9 @@ int64_t gdr_chunk_workspace_bytes(const gdr_args* a) {
   const int rc = check_shape(a, true);
   if (rc) return rc;
   g_last_error.clear();
-  return gdr::chunk_workspace_bytes(*a);
+  // Read from the sizes alone (no dtype): key dims the chunk kernels do not take run the sequential path, which needs
+  // no workspace; so do fp32 calls, which ignore the one they are given.
+  return (a->key_dim == 64 || a->key_dim == 128) ? gdr::chunk_workspace_bytes(*a) : 0;
 }
 
 int gdr_chunk_fwd(const gdr_args* a, hipStream_t stream) { return chunk_fwd(a, nullptr, stream); }
@@ -452,6 +494,7 @@ int gdr_chunk_fwd_noalloc(const gdr_args* a, hipStream_t stream) {
   if (rc) return rc;
   if (a->workspace) return fail(GDR_ERR_INVALID, "gdr_chunk_fwd_noalloc: workspace must be NULL (the library's "
                                 "device scratch is used)");
+  if (chunk_sequential(a)) return chunk_fwd_sequential(a, nullptr, stream);  // no scratch needed
   const int64_t need = gdr::chunk_workspace_bytes(*a);
   if (need > GDR_NOALLOC_SCRATCH_BYTES)
     return fail(GDR_ERR_UNSUPPORTED, "gdr_chunk_fwd_noalloc: this call needs %lld bytes of scratch, above the "
@@ -475,9 +518,10 @@ int gdr_chunk_fwd_fused(const gdr_args* a, const gdr_prologue* pro, hipStream_t 
 }
 
 int64_t gdr_chunk_bwd_workspace_bytes(const gdr_args* a) {
-  const int rc = check_shape(a, true);
+  int rc = check_shape(a, true);
   if (rc) return rc;
   if (a->cu_seqlens) return fail(GDR_ERR_UNSUPPORTED, "the chunk backward does not take packed varlen input");
+  if ((rc = check_bwd_shape(a))) return rc;
   g_last_error.clear();
   return gdr::chunk_bwd_layout(*a).total;
 }
@@ -499,6 +543,7 @@ int gdr_chunk_fwd_train(const gdr_args* a, void* workspace, int64_t workspace_by
   int rc = check_common(a, true, true);
   if (rc) return rc;
   if (a->cu_seqlens) return fail(GDR_ERR_UNSUPPORTED, "the chunk backward does not take packed varlen input");
+  if ((rc = check_bwd_shape(a))) return rc;
   if (a->q.dtype != GDR_BF16 || a->k.dtype != GDR_BF16 || a->v.dtype != GDR_BF16)
     return fail(GDR_ERR_UNSUPPORTED, "the chunk backward reads bf16 q, k, v (got dtype codes %d, %d, %d)", a->q.dtype,
                 a->k.dtype, a->v.dtype);

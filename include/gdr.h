@@ -89,9 +89,13 @@ typedef struct gdr_args {
  * (pad_sequence + chunk_cumsum + kernel matrices + WY representation + state scan + output, six launches and
  * a [B,H,NC+1,K,V] States buffer in the reference).  With a workspace it is two launches on `stream`: a
  * chunk-parallel preparation kernel that writes one record per (chunk, head) into the workspace, then the state
- * scan that reads them; with workspace NULL it is one slower launch that needs no scratch.  q, k, v must be all
- * bf16 or all f16 (the MFMA operand type; the Python layer casts); out may be bf16, f16 or f32.
- * Supports K in {64, 128}, V a multiple of 64, any T >= 0, and packed varlen input through cu_seqlens. */
+ * scan that reads them; with workspace NULL it is one slower launch that needs no scratch.  On that path q, k, v
+ * are all bf16 or all f16 (the MFMA operand type; the Python layer casts), K is 64 or 128 and V a multiple of 64.
+ * Two kinds of call take the sequential path instead -- one launch of the recurrent kernel over every token of each
+ * sequence, the state, every product and every sum in fp32, no workspace used: q, k, v all f32 (the reference's
+ * kernels take f32 dot operands for f32 inputs), and K in {32, 192, 256} (key dims the chunk kernels are not built
+ * for; the reference's chunk kernels take any multiple of 64), with q, k, v all bf16 or all f32 and V a multiple of
+ * 32.  out may be bf16, f16 or f32.  Any T >= 0, and packed varlen input through cu_seqlens on both paths. */
 int gdr_chunk_fwd(const gdr_args* args, hipStream_t stream);
 
 /* Fused layer prologue for gdr_chunk_fwd_fused: the per-token work the reference's KDA layer does in PyTorch before
@@ -135,7 +139,8 @@ int gdr_chunk_fwd_fused(const gdr_args* args, const gdr_prologue* pro, hipStream
  * that the chunk-parallel preparation kernel writes and the state-scan kernel reads: the reference keeps the
  * same kind of intermediates (gate cumsum, P, A, W, U, States) in tensors it allocates per call
  * (src/ops/kimi_delta_attention.py:540-553).  For B=4, T=4096, H=16, K=V=128 it is 291.5 MB (71,168 bytes per
- * chunk and head). */
+ * chunk and head).  The size does not depend on dtypes; it is 0 for key dims the chunk kernels do not take (the
+ * sequential path needs no workspace, and ignores one it is given, as f32 calls do). */
 int64_t gdr_chunk_workspace_bytes(const gdr_args* args);
 
 /* Size of the device scratch behind gdr_chunk_fwd_noalloc (128 MiB per GPU). */
@@ -204,7 +209,8 @@ int gdr_chunk_bwd_saved(const gdr_args* args, const gdr_grads* grads, void* work
  *   recurrent_gated_linear_attention   src/ops/gated_linear_attention.py:461-483 (kernel :30-56)
  *   recurrent_deltanet                 src/ops/deltanet.py:423-445 (kernel :30-57)
  * q, k, v must share one dtype, bf16 or f32 (the Python layer widens mixed or f16 inputs to f32, exactly); out may
- * be bf16, f16 or f32.  Supports K in {64, 128}, V a multiple of 32, any T >= 1 (cu_seqlens must be NULL). */
+ * be bf16, f16 or f32.  Supports K in {32, 64, 128, 192, 256} (the reference's kernel takes any power-of-two head
+ * dim, :46), V a multiple of 32, any T >= 0 (cu_seqlens must be NULL; packed input runs through gdr_chunk_fwd). */
 int gdr_recurrent_fwd(const gdr_args* args, hipStream_t stream);
 
 /* Multi-token verify for speculative decoding: gdr_recurrent_fwd over a block of T tokens (the pending token plus
