@@ -152,9 +152,13 @@ __device__ __forceinline__ float conv4_silu1(const __bf16* x0, int64_t x_st, int
 // chunk c ^ (r mod K / 8), copied with global_load_lds_dwordx4: the permutation is applied to the source addresses,
 // since the copy lands lane i at base + 16 i).  Lane (l16, g4) ends with channels 16 t + 4 g4 + i of token 16 j + l16;
 // the values go to the fp32 LDS rows `gst` (row pitch K + 4), from which every lane later reads its own row.
-template <int K>
+// `after_first_block()` runs once the first block of z and W has arrived, before its products: the caller issues its
+// own row loads there, so that their latency overlaps the gate's products instead of following them (the
+// barriers below order LDS only and do not wait for those loads).
+template <int K, typename AfterFirstBlock>
 __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h, const __bf16* zchunk, int64_t z_st,
-                                                  int last_row, float* gst, __bf16* zs, int wave, int l16, int g4) {
+                                                  int last_row, float* gst, __bf16* zs, int wave, int l16, int g4,
+                                                  const AfterFirstBlock& after_first_block) {
   constexpr int CT = K / 64;          // 16-channel tiles per wave
   constexpr int RB = K, C16 = RB / 8;  // R per LDS block, 16-byte chunks per staged row
   const int R = pro.rank, ch0 = wave * (K / 4), lane = threadIdx.x & 63;
@@ -164,7 +168,22 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
   for (int t = 0; t < CT; ++t)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[t][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  // A_log and the bias are requested first, and each block's W fragments before its z rows: one wait then covers
+  // every load of a block, instead of a memory round trip per dependent fragment.
+  const float a_log_h = pro.a_log[h];
+  float4 bias[CT];
+#pragma unroll
+  for (int t = 0; t < CT; ++t) {
+    bias[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (pro.gate_bias) bias[t] = *reinterpret_cast<const float4*>(pro.gate_bias + size_t(h) * K + ch0 + 16 * t + 4 * g4);
+  }
   for (int r0 = 0; r0 < R; r0 += RB) {  // the accumulators start at zero right before this loop
+    bf16x8 wa[CT][RB / 32];
+#pragma unroll
+    for (int t = 0; t < CT; ++t)
+#pragma unroll
+      for (int s = 0; s < RB / 32; ++s)
+        wa[t][s] = *reinterpret_cast<const bf16x8*>(w + size_t(16 * t) * R + min(r0 + 32 * s, R - 32));
     // stage z[0:64][r0 : r0 + RB] (columns past R read column R - 8 and meet zero W operands below)
 #pragma unroll
     for (int k = 0; k < 64 * C16 / 256; ++k) {
@@ -174,7 +193,8 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
       lds_dma16(zchunk + int64_t(min(row, last_row)) * z_st + col, zs + 8 * 64 * (4 * k + wave));
     }
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    lds_barrier();
+    if (r0 == 0) after_first_block();
 #pragma unroll
     for (int s = 0; s < RB / 32; ++s) {
       const bool live = r0 + 32 * s < R;
@@ -186,25 +206,23 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
       }
 #pragma unroll
       for (int t = 0; t < CT; ++t) {
-        bf16x8 wa = *reinterpret_cast<const bf16x8*>(w + size_t(16 * t) * R + min(r0 + 32 * s, R - 32));
-        if (!live) wa = bf16x8{};
+        const bf16x8 wf = live ? wa[t][s] : bf16x8{};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[t][j] = mfma32(wa, zb[j], acc[t][j]);
+        for (int j = 0; j < 4; ++j) acc[t][j] = mfma32(wf, zb[j], acc[t][j]);
       }
     }
-    __syncthreads();  // every wave is done with this block of zs
+    lds_barrier();  // every wave is done with this block of zs
   }
-  const float neg_a = -__builtin_amdgcn_exp2f(pro.a_log[h] * kLog2e);
+  const float neg_a = -__builtin_amdgcn_exp2f(a_log_h * kLog2e);
 #pragma unroll
   for (int t = 0; t < CT; ++t) {
     const int ch = ch0 + 16 * t + 4 * g4;
-    float4 bias = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (pro.gate_bias) bias = *reinterpret_cast<const float4*>(pro.gate_bias + size_t(h) * K + ch);
+    const float4 bias_t = bias[t];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float4 g = make_float4(
-          neg_a * softplus_f32(acc[t][j][0] + bias.x), neg_a * softplus_f32(acc[t][j][1] + bias.y),
-          neg_a * softplus_f32(acc[t][j][2] + bias.z), neg_a * softplus_f32(acc[t][j][3] + bias.w));
+          neg_a * softplus_f32(acc[t][j][0] + bias_t.x), neg_a * softplus_f32(acc[t][j][1] + bias_t.y),
+          neg_a * softplus_f32(acc[t][j][2] + bias_t.z), neg_a * softplus_f32(acc[t][j][3] + bias_t.w));
       *reinterpret_cast<float4*>(gst + (16 * j + l16) * (K + 4) + ch) = g;
     }
   }
@@ -350,9 +368,21 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
     // The gate rows are computed into the KAP / KD region, which nothing uses before step 3b (after two barriers).
     const __bf16* zchunk = static_cast<const __bf16*>(pro.gate_lowrank.ptr) + bidx * pro.gate_lowrank.stride_b +
                            int64_t(bos + c * kChunk) * pro.gate_lowrank.stride_t;
+    auto issue_rows = [&]() {  // without the in-kernel convolution: this lane's q, k rows and the first V pass
+      if constexpr (!kConv) {
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+          const int ch = 32 * kk + 8 * g4;
+          qraw[kk] = *reinterpret_cast<const uint4*>(x.qp + tc * x.q_st + ch);
+          kraw[kk] = *reinterpret_cast<const uint4*>(x.kp + tc * x.k_st + ch);
+        }
+        load_v_pass(0);
+      }
+    };
     lowrank_gate_rows<K>(pro, h, zchunk, pro.gate_lowrank.stride_t, len - 1 - c * kChunk,
-                         reinterpret_cast<float*>(smem), reinterpret_cast<__bf16*>(smem + L::SC), wave, l16, g4);
-    __syncthreads();
+                         reinterpret_cast<float*>(smem), reinterpret_cast<__bf16*>(smem + L::SC), wave, l16, g4,
+                         issue_rows);
+    lds_barrier();
   }
   if constexpr (kConv) {
     // The convolved q, k rows are staged in the KAP / KD tiles (bf16 [64][KP]; free until step 3b): unit u covers
@@ -391,7 +421,7 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
     if constexpr (kConv) {
       qraw[kk] = *reinterpret_cast<const uint4*>(kap + (16 * p + l16) * KP + ch);
       kraw[kk] = *reinterpret_cast<const uint4*>(kd + (16 * p + l16) * KP + ch);
-    } else {
+    } else if constexpr (!kLowRank) {  // (with the low-rank gate they were requested during its products)
       qraw[kk] = *reinterpret_cast<const uint4*>(x.qp + tc * x.q_st + ch);
       kraw[kk] = *reinterpret_cast<const uint4*>(x.kp + tc * x.k_st + ch);
     }
@@ -454,7 +484,7 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
       kraw[kk] = *reinterpret_cast<const uint4*>(&nk);
     }
   }
-  load_v_pass(0);
+  if constexpr (!kLowRank || kConv) load_v_pass(0);
 
   // ---- 2. in-block inclusive cumsum of the log2 gate over the 16 rows (one DPP row per channel group) ----
   if constexpr (kGate) {
