@@ -18,7 +18,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.join(_HERE, "libgdr.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 PRO_NORM_QK, PRO_BETA_LOGITS, PRO_GATE_LOWRANK, PRO_CONV = 1, 2, 4, 8
 
 KDA, GDN, GLA, DELTANET = 0, 1, 2, 3
@@ -94,6 +94,19 @@ class GdrAttentionArgs(ctypes.Structure):
         ("v", GdrTensor),
         ("out", GdrTensor),
         ("cu_seqlens", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+    ]
+
+
+class GdrAttentionGrads(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("d_out", GdrTensor),
+        ("d_q", GdrTensor),
+        ("d_k", GdrTensor),
+        ("d_v", GdrTensor),
+        ("delta", ctypes.c_void_p),
     ]
 
 
@@ -166,6 +179,8 @@ EXPORTS = {
     "gdr_recurrent_commit_verify": (ctypes.c_int, [ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p,
                                                    ctypes.POINTER(GdrArgs), ctypes.c_void_p, ctypes.c_void_p]),
     "gdr_attention_fwd": (ctypes.c_int, [ctypes.POINTER(GdrAttentionArgs), ctypes.c_void_p]),
+    "gdr_attention_bwd": (ctypes.c_int, [ctypes.POINTER(GdrAttentionArgs), ctypes.POINTER(GdrAttentionGrads),
+                                         ctypes.c_void_p]),
     "gdr_short_conv_fwd": (ctypes.c_int, [ctypes.POINTER(GdrConvArgs), ctypes.c_void_p]),
     "gdr_norm_gate_fwd": (ctypes.c_int, [ctypes.POINTER(GdrNormGateArgs), ctypes.c_void_p]),
     "gdr_last_error": (ctypes.c_char_p, []),
@@ -375,8 +390,7 @@ def _view3(x: torch.Tensor, name: str) -> GdrTensor:
     return view
 
 
-def attention(q, k, v, out, scale, cu_seqlens, device) -> None:
-    """Enqueue gdr_attention_fwd on torch's current stream."""
+def _attention_args(q, k, v, out, scale, cu_seqlens, lse) -> GdrAttentionArgs:
     args = GdrAttentionArgs()
     args.abi_version = ABI_VERSION
     args.batch, args.heads, args.seq_len, args.head_dim = q.shape[0], q.shape[1], q.shape[2], q.shape[3]
@@ -386,9 +400,32 @@ def attention(q, k, v, out, scale, cu_seqlens, device) -> None:
     if cu_seqlens is not None:
         args.cu_seqlens = cu_seqlens.data_ptr()
         args.n_seqs = cu_seqlens.numel() - 1
+    args.lse = lse.data_ptr() if lse is not None else None
+    return args
+
+
+def attention(q, k, v, out, scale, cu_seqlens, device, lse=None) -> None:
+    """Enqueue gdr_attention_fwd on torch's current stream (writing the row log-sum-exp into `lse`, fp32 [B, H, T],
+    when given)."""
+    args = _attention_args(q, k, v, out, scale, cu_seqlens, lse)
     lib = load_library()
     stream = torch.cuda.current_stream(device).cuda_stream
     _check("gdr_attention_fwd", lib.gdr_attention_fwd(ctypes.byref(args), ctypes.c_void_p(stream)))
+
+
+def attention_bwd(q, k, v, out, lse, scale, cu_seqlens, d_out, d_q, d_k, d_v, delta, device) -> None:
+    """Enqueue gdr_attention_bwd on torch's current stream: d_q, d_k, d_v from the forward's q, k, v, out and lse
+    and the incoming d_out; `delta` (fp32 [B, H, T]) is scratch."""
+    args = _attention_args(q, k, v, out, scale, cu_seqlens, lse)
+    grads = GdrAttentionGrads()
+    grads.abi_version = ABI_VERSION
+    grads.d_out, grads.d_q = _view(d_out, "d_out"), _view(d_q, "d_q")
+    grads.d_k, grads.d_v = _view(d_k, "d_k"), _view(d_v, "d_v")
+    grads.delta = delta.data_ptr()
+    lib = load_library()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    _check("gdr_attention_bwd", lib.gdr_attention_bwd(ctypes.byref(args), ctypes.byref(grads),
+                                                      ctypes.c_void_p(stream)))
 
 
 def short_conv(x, out, weight, state_in, state_out, cu_seqlens, silu, device) -> None:

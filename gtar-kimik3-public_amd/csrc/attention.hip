@@ -19,57 +19,25 @@
 // tiles only, and the row sums come out of the MFMA (all-ones A operand) from the same rounded probabilities as
 // P V (uniform branches around VALU work; no MFMA sits under a data-dependent branch).  K tiles run one ahead of V
 // tiles, so each tile's exponentials interleave with the next tile's score MFMAs in one basic block.
-#include "chunk_common.h"
+#include "attention_common.h"
 #include "varlen_index.h"
 #include "gdr_internal.h"
 
 namespace gdr {
 namespace {
 
+using attn::cat;
+using attn::Mma;
+using attn::short4;
 using chunk::kLog2e;
 using chunk::lds_dma16;
-using chunk::pack4;
 
 constexpr int kBM = 128;  // query rows per workgroup
-constexpr int kBN = 64;   // keys per LDS tile
-constexpr int kAttnThreads = 256;
+constexpr int kBN = attn::kTile;  // keys per LDS tile
+constexpr int kAttnThreads = attn::kThreads;
 constexpr int kRB = 2;  // 16-row query blocks per wave
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kLazy = 8.f;  // log2 of the largest probability before the accumulators are rebased
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef short short4 __attribute__((ext_vector_type(4)));
-
-template <typename T>
-struct Mma;
-template <>
-struct Mma<__bf16> {
-  using v8 = bf16x8;
-  using v4 = bf16x4;
-  static __device__ __forceinline__ floatx4 run(v8 a, v8 b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ v4 pack(floatx4 x) { return pack4(x); }
-};
-template <>
-struct Mma<_Float16> {
-  using v8 = f16x8;
-  using v4 = f16x4;
-  static __device__ __forceinline__ floatx4 run(v8 a, v8 b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ v4 pack(floatx4 x) {
-    return v4{static_cast<_Float16>(x[0]), static_cast<_Float16>(x[1]), static_cast<_Float16>(x[2]),
-              static_cast<_Float16>(x[3])};
-  }
-};
-
-template <typename V4, typename V8>
-__device__ __forceinline__ V8 cat(V4 lo, V4 hi) {
-  return V8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
 
 template <int D, typename T>
 __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gdr_attention_args a, int nqb) {
@@ -269,15 +237,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
   // "lgkmcnt(4)" after the next tile's four reads covers this tile's reads whatever else the compiler interleaves.
   auto pv = [&](uint32_t vt, const V8 (&pf)[kRB][2]) {
     short4 x[2][4];
-    auto rd = [&](int t, short4 (&r)[4]) {
-      asm volatile(
-          "ds_read_b64_tr_b16 %0, %4\n\t"
-          "ds_read_b64_tr_b16 %1, %4 offset:%5\n\t"
-          "ds_read_b64_tr_b16 %2, %4 offset:%6\n\t"
-          "ds_read_b64_tr_b16 %3, %4 offset:%7"
-          : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-          : "v"(vt + 2 * voff[t]), "i"(2 * 16 * D), "i"(2 * 32 * D), "i"(2 * 48 * D));
-    };
+    auto rd = [&](int t, short4 (&r)[4]) { attn::tr_read4<D>(vt + 2 * voff[t], r); };
     rd(0, x[0]);
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
@@ -300,7 +260,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
 #pragma unroll
       for (int b = 0; b < kRB; ++b) lsum[b] = M::run(ones, pf[b][s2], lsum[b]);
   };
-  const uint32_t vlds = static_cast<uint32_t>((uintptr_t)(__attribute__((address_space(3))) const unsigned char*)vs);
+  const uint32_t vlds = attn::lds_addr(vs);
 
   issue(kp, a.k.stride_t, koffs, ks, 0);
   issue(vp, a.v.stride_t, voffs, vs, 0);
@@ -337,6 +297,14 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attention_fwd_kernel(const gd
     pv(vlds + (kb & 1) * TILE * 2, pf);
   }
 
+  // The row log-sum-exp of the scaled scores in log2 units, m + log2(row sum): the backward's probabilities are
+  // 2^(c s - lse), the same normalisation as the output's.
+  if (a.lse && g4 == 0) {
+    float* lp = a.lse + (int64_t(bidx) * H + h) * a.seq_len + bos;
+#pragma unroll
+    for (int b = 0; b < kRB; ++b)
+      if (qpos[b] < len) lp[qpos[b]] = m[b] + __builtin_amdgcn_logf(lsum[b][0]);
+  }
 #pragma unroll
   for (int b = 0; b < kRB; ++b) {
     if (qpos[b] < len) {

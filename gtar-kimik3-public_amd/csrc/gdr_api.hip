@@ -382,7 +382,10 @@ int gdr_recurrent_commit_verify(const gdr_args* prev, const float* prev_updates,
   return GDR_OK;
 }
 
-int gdr_attention_fwd(const gdr_attention_args* a, hipStream_t stream) {
+namespace {
+
+// The forward's arguments (no pointer dereferenced); the views in `views` share q's 16-bit dtype, rows 16-byte aligned.
+int check_attention(const gdr_attention_args* a, const gdr_tensor* const* views, const char* const* names, int nviews) {
   if (!a) return fail(GDR_ERR_INVALID, "args is NULL");
   if (a->abi_version != GDR_ABI_VERSION)
     return fail(GDR_ERR_INVALID, "abi_version %d, library implements %d", a->abi_version, GDR_ABI_VERSION);
@@ -393,18 +396,43 @@ int gdr_attention_fwd(const gdr_attention_args* a, hipStream_t stream) {
     return fail(GDR_ERR_UNSUPPORTED, "head dim %d not supported (64 or 128)", a->head_dim);
   if (a->cu_seqlens && (a->batch != 1 || a->n_seqs < 1))
     return fail(GDR_ERR_INVALID, "cu_seqlens requires batch == 1 and n_seqs >= 1");
+  if (reinterpret_cast<uintptr_t>(a->lse) % 4) return fail(GDR_ERR_INVALID, "lse must be 4-byte aligned");
   int rc;
-  const gdr_tensor* views[] = {&a->q, &a->k, &a->v, &a->out};
-  const char* names[] = {"query", "key", "value", "out"};
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < nviews; ++i) {
     if ((rc = check_view(*views[i], names[i], true, false))) return rc;
     if (views[i]->dtype != a->q.dtype)
-      return fail(GDR_ERR_UNSUPPORTED, "%s: q, k, v and out share one dtype", names[i]);
+      return fail(GDR_ERR_UNSUPPORTED, "%s: q, k, v, out (and the gradients) share one dtype", names[i]);
     if ((rc = check_rows16(*views[i], names[i]))) return rc;
   }
   if (a->q.dtype == GDR_F32) return fail(GDR_ERR_UNSUPPORTED, "attention reads bf16 or f16 (the MFMA operand types)");
+  return GDR_OK;
+}
+
+}  // namespace
+
+int gdr_attention_fwd(const gdr_attention_args* a, hipStream_t stream) {
+  const gdr_tensor* views[] = {a ? &a->q : nullptr, a ? &a->k : nullptr, a ? &a->v : nullptr, a ? &a->out : nullptr};
+  const char* names[] = {"query", "key", "value", "out"};
+  if (const int rc = check_attention(a, views, names, 4)) return rc;
   hipError_t e = gdr::launch_attention(*a, stream);
   if (e != hipSuccess) return fail(GDR_ERR_HIP, "attention launch failed: %s", hipGetErrorString(e));
+  g_last_error.clear();
+  return GDR_OK;
+}
+
+int gdr_attention_bwd(const gdr_attention_args* a, const gdr_attention_grads* g, hipStream_t stream) {
+  if (!g) return fail(GDR_ERR_INVALID, "grads is NULL");
+  if (g->abi_version != GDR_ABI_VERSION)
+    return fail(GDR_ERR_INVALID, "grads abi_version %d, library implements %d", g->abi_version, GDR_ABI_VERSION);
+  const gdr_tensor* views[] = {a ? &a->q : nullptr, a ? &a->k : nullptr, a ? &a->v : nullptr, a ? &a->out : nullptr,
+                               &g->d_out, &g->d_q, &g->d_k, &g->d_v};
+  const char* names[] = {"query", "key", "value", "out", "d_out", "d_q", "d_k", "d_v"};
+  if (const int rc = check_attention(a, views, names, 8)) return rc;
+  if (!a->lse) return fail(GDR_ERR_INVALID, "lse is NULL: the backward reads the forward's row log-sum-exp");
+  if (!g->delta || reinterpret_cast<uintptr_t>(g->delta) % 4)
+    return fail(GDR_ERR_INVALID, "delta must be a non-NULL, 4-byte aligned fp32 [B][H][T] buffer");
+  hipError_t e = gdr::launch_attention_bwd(*a, *g, stream);
+  if (e != hipSuccess) return fail(GDR_ERR_HIP, "attention backward launch failed: %s", hipGetErrorString(e));
   g_last_error.clear();
   return GDR_OK;
 }

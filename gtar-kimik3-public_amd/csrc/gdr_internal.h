@@ -37,6 +37,7 @@ hipError_t launch_chunk(const gdr_args& a, hipStream_t stream);
 
 // Causal grouped-query attention and the segment-aware short convolution; arguments validated.
 hipError_t launch_attention(const gdr_attention_args& a, hipStream_t stream);
+hipError_t launch_attention_bwd(const gdr_attention_args& a, const gdr_attention_grads& g, hipStream_t stream);
 hipError_t launch_short_conv(const gdr_conv_args& a, hipStream_t stream);
 // The layer's output epilogue (RMSNorm x SiLU gate); arguments validated.
 hipError_t launch_norm_gate(const gdr_norm_gate_args& a, hipStream_t stream);

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GDR_ABI_VERSION 7
+#define GDR_ABI_VERSION 8
 
 typedef enum gdr_variant { GDR_KDA = 0, GDR_GDN = 1, GDR_GLA = 2, GDR_DELTANET = 3 } gdr_variant;
 
@@ -244,7 +244,7 @@ int gdr_recurrent_commit(const gdr_args* args, const float* updates, const int32
 int gdr_recurrent_commit_verify(const gdr_args* prev, const float* prev_updates, const int32_t* accepted,
                                 const gdr_args* args, float* updates, hipStream_t stream);
 
-/* Causal softmax attention of the hybrid stack's attention layer (grouped-query; forward only). */
+/* Causal softmax attention of the hybrid stack's attention layer (grouped-query), forward and backward. */
 typedef struct gdr_attention_args {
   int32_t abi_version;       /* must equal GDR_ABI_VERSION */
   int32_t batch;             /* B; must be 1 when cu_seqlens is given */
@@ -258,6 +258,10 @@ typedef struct gdr_attention_args {
                                 aligned */
   gdr_tensor out;            /* [B, H, T, D], the dtype of q */
   const int32_t* cu_seqlens; /* device int32 [n_seqs + 1] packed-sequence offsets, or NULL */
+  float* lse;                /* device fp32 [B][H][T], 4-byte aligned, or NULL.  Forward: when not NULL, receives
+                                each query row's log-sum-exp of its scaled scores in log2 units,
+                                log2 sum_s 2^(scale log2(e) q.k_s), for the backward.  Backward: the forward's,
+                                read. */
 } gdr_attention_args;
 
 /* O = softmax(scale Q K^T + causal mask) V per (sequence, query head), with attention confined to each packed
@@ -265,6 +269,25 @@ typedef struct gdr_attention_args {
  * kernel :24-71, reached from src/layers/attention.py:113), which takes no packed input: the reference pads
  * batches (flash_attention_2.py:155-158).  Supports D in {64, 128}, any T >= 1. */
 int gdr_attention_fwd(const gdr_attention_args* args, hipStream_t stream);
+
+/* Gradients of gdr_attention_fwd. */
+typedef struct gdr_attention_grads {
+  int32_t abi_version; /* must equal GDR_ABI_VERSION */
+  int32_t reserved;
+  gdr_tensor d_out;    /* [B, H, T, D], the dtype of q, rows 16-byte aligned */
+  gdr_tensor d_q;      /* [B, H, T, D], the dtype of q, rows 16-byte aligned; written */
+  gdr_tensor d_k, d_v; /* [B, kv_heads, T, D], the dtype of q, rows 16-byte aligned; written, each summed over the
+                          query heads of its group */
+  float* delta;        /* device fp32 [B][H][T] scratch, 4-byte aligned: rowsum(out * d_out), written and then read
+                          by the call */
+} gdr_attention_grads;
+
+/* dQ, dK, dV of O = softmax(scale Q K^T + causal mask) V given dO.  `args` is the forward call's (q, k, v, out, the
+ * lse it wrote, scale, cu_seqlens).  Replaces FlashAttention.backward (src/ops/flash_attention_2.py:180-207: the
+ * delta preprocessing :63-75, the dK/dV kernel :77-117 and the dQ kernel :119-151).  Two launches on `stream`: per
+ * 128-row query block the row sums delta and dQ, then per 64-row key block of a key/value head dK and dV over every
+ * query of its group's heads from the diagonal on.  Supports what gdr_attention_fwd supports. */
+int gdr_attention_bwd(const gdr_attention_args* args, const gdr_attention_grads* grads, hipStream_t stream);
 
 /* Depthwise causal convolution + SiLU of the layers' short convolution, segment-aware. */
 typedef struct gdr_conv_args {

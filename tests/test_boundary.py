@@ -45,7 +45,8 @@ def test_struct_layout_matches_header(tmp_path):
     lines += [f'printf("p.{f} %zu\\n", offsetof(gdr_prologue, {f}));' for f, _ in lib.GdrPrologue._fields_]
     lines += ['printf("p.size %zu\\n", sizeof(gdr_prologue));']
     for tag, struct, cls in (("a", "gdr_attention_args", lib.GdrAttentionArgs), ("c", "gdr_conv_args", lib.GdrConvArgs),
-                             ("n", "gdr_norm_gate_args", lib.GdrNormGateArgs)):
+                             ("n", "gdr_norm_gate_args", lib.GdrNormGateArgs),
+                             ("ag", "gdr_attention_grads", lib.GdrAttentionGrads)):
         lines += [f'printf("{tag}.{f} %zu\\n", offsetof({struct}, {f}));' for f, _ in cls._fields_]
         lines += [f'printf("{tag}.size %zu\\n", sizeof({struct}));']
     lines += ["return 0; }"]
@@ -67,7 +68,8 @@ def test_struct_layout_matches_header(tmp_path):
     for f, _ in lib.GdrPrologue._fields_:
         assert int(offsets["p." + f]) == getattr(lib.GdrPrologue, f).offset, f
     assert int(offsets["p.size"]) == ctypes.sizeof(lib.GdrPrologue)
-    for tag, cls in (("a", lib.GdrAttentionArgs), ("c", lib.GdrConvArgs), ("n", lib.GdrNormGateArgs)):
+    for tag, cls in (("a", lib.GdrAttentionArgs), ("c", lib.GdrConvArgs), ("n", lib.GdrNormGateArgs),
+                     ("ag", lib.GdrAttentionGrads)):
         for f, _ in cls._fields_:
             assert int(offsets[f"{tag}.{f}"]) == getattr(cls, f).offset, f
         assert int(offsets[f"{tag}.size"]) == ctypes.sizeof(cls)
@@ -308,6 +310,28 @@ def test_attention_and_conv_reject_bad_arguments_without_a_gpu():
         view.ptr, view.dtype = off, lib.F32
     assert so.gdr_attention_fwd(ctypes.byref(a), None) == -2
     assert b"bf16 or f16" in so.gdr_last_error()
+    # the backward: the forward's checks plus the gradients, the saved lse and the delta scratch
+    g = lib.GdrAttentionGrads()
+    g.abi_version = lib.ABI_VERSION
+    assert so.gdr_attention_bwd(ctypes.byref(a), None, None) == -1
+    assert b"grads is NULL" in so.gdr_last_error()
+    for name, off in (("q", 256), ("k", 512), ("v", 768), ("out", 1024)):
+        getattr(a, name).dtype = lib.BF16
+    for name, off in (("d_out", 1280), ("d_q", 1536), ("d_k", 1792), ("d_v", 2048)):
+        view = getattr(g, name)
+        view.ptr, view.dtype = off, lib.BF16
+    g.d_v.dtype = lib.F16
+    assert so.gdr_attention_bwd(ctypes.byref(a), ctypes.byref(g), None) == -2
+    assert b"d_v" in so.gdr_last_error()
+    g.d_v.dtype = lib.BF16
+    assert so.gdr_attention_bwd(ctypes.byref(a), ctypes.byref(g), None) == -1
+    assert b"lse is NULL" in so.gdr_last_error()
+    a.lse = 4096
+    assert so.gdr_attention_bwd(ctypes.byref(a), ctypes.byref(g), None) == -1
+    assert b"delta" in so.gdr_last_error()
+    a.lse = 4098
+    assert so.gdr_attention_fwd(ctypes.byref(a), None) == -1
+    assert b"lse must be 4-byte aligned" in so.gdr_last_error()
     c = lib.GdrConvArgs()
     c.abi_version = lib.ABI_VERSION
     c.batch, c.seq_len, c.channels, c.kernel_size = 1, 8, 64, 9
@@ -324,7 +348,7 @@ def test_stack_ops_refuse_cpu_tensors_and_gradients():
     q = torch.randn(1, 2, 8, 64)
     with pytest.raises(ValueError, match="GPU"):
         gdr.flash_attention(q, q, q)
-    with pytest.raises(NotImplementedError, match="forward only"):
+    with pytest.raises(ValueError, match="GPU"):  # differentiable, but never on the CPU
         gdr.flash_attention(q.requires_grad_(), q, q)
     with pytest.raises(ValueError, match="GPU"):
         gdr.short_convolution(torch.randn(1, 8, 64), torch.randn(64, 1, 4))
