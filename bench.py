@@ -24,7 +24,7 @@ One JSON line on stdout:
     and the KDA op's share of the time.
   * attention: the stack's causal attention layer alone on the packed configuration (16 query / 8 key-value heads,
     head dim 128, bf16): ms per call, TFLOP/s over the causal FLOPs 4 H D L (L + 1) / 2 per sequence, and the
-    fraction of dense bf16 MFMA peak.
+    fraction of dense bf16 MFMA peak; then its backward alone (gdr_attention_bwd), over 2.5x those FLOPs.
   * train: the prefill configuration under torch.autograd, the training forward (gdr_chunk_fwd_train) then the
     backward (gdr_chunk_bwd_saved), steps queued back to back, with the backward's algorithmic bytes and HBM
     fraction.
@@ -457,9 +457,26 @@ def bench_attention(gdr, workloads, torch, steps, warmup):
     ms = start.elapsed_time(stop) / steps
     flops = sum(4 * H * D * n * (n + 1) / 2 for n in lengths)
     tflops = flops / (ms * 1e-3) / 1e12
+    # The backward alone (gdr_attention_bwd: the dQ launch, then the dK / dV launch), replayed on one retained graph
+    # with a fixed output gradient.  Its algorithmic FLOPs are the usual five causal products (S recomputed, dP, dV,
+    # dK, dQ: 2.5x the forward's); the kernels form S and dP in both launches, seven products in all.
+    leaves = [x.clone().requires_grad_() for x in (q, k, v)]
+    out = gdr.flash_attention(*leaves, cu_seqlens=cu)
+    d_out = torch.randn(out.shape, device="cuda", generator=g).bfloat16()
+    for _ in range(warmup):
+        torch.autograd.grad(out, leaves, d_out, retain_graph=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        torch.autograd.grad(out, leaves, d_out, retain_graph=True)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    bwd_ms = start.elapsed_time(stop) / steps
+    bwd_tflops = 2.5 * flops / (bwd_ms * 1e-3) / 1e12
     return {"workload": "packed_causal_attention", "n_seqs": len(lengths), "tokens": tokens, "heads": H,
             "kv_heads": Hkv, "head_dim": D, "ms_per_call": round(ms, 4), "tflops": round(tflops, 1),
-            "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+            "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "backward_ms_per_call": round(bwd_ms, 4),
+            "backward_tflops": round(bwd_tflops, 1), "backward_mfma_frac": round(bwd_tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
 
 
 def bench_stack(gdr, workloads, torch, steps, warmup):
