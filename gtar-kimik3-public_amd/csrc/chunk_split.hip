@@ -83,17 +83,19 @@ __device__ __forceinline__ float softplus_f32(float x) {
   return fmaxf(x, 0.f) + l1p;
 }
 
-// The fused prologue's short convolution (ShortConvolution, src/layers/short_convolution.py:11-20; width 4):
-// silu(sum_{j < 4} w[c][j] x[t - 3 + j][c]) for 8 consecutive channels at the 4 sequence rows r0 .. r0 + 3, accumulated
-// in fp32 and rounded once to bf16 (as gdr_short_conv_fwd).  The 7 input rows r0 - 3 .. r0 + 3 are loaded once;
-// rows before the sequence come from its conv state [C][3] (`st8` points at the first of the 8 channels' rows) or are
-// zero, and rows past `last` (the sequence's last row) read row `last` (their outputs are masked by the caller).
-// `x0` is row 0 of the sequence at the first channel, `w8` the 8 channels' weight rows ([8][4], 64 contiguous bytes).
-__device__ __forceinline__ void conv4_silu8x4(const __bf16* x0, int64_t x_st, int r0, int last, const __bf16* w8,
-                                              const __bf16* st8, uint4 (&out)[4]) {
-  uint32_t w[16];  // packed bf16 pairs: weight (e, j) is bf16 number 4 e + j
+// The fused prologue's short convolution (ShortConvolution, src/layers/short_convolution.py:11-20) of width W:
+// silu(sum_{j < W} w[c][j] x[t - W + 1 + j][c]) for 8 consecutive channels at the 4 sequence rows r0 .. r0 + 3,
+// accumulated in fp32 and rounded once to bf16 (as gdr_short_conv_fwd).  The W + 3 input rows r0 - W + 1 .. r0 + 3
+// are loaded once; rows before the sequence come from its conv state [C][W - 1] (`st8` points at the first of the 8
+// channels' rows) or are zero, and rows past `last` (the sequence's last row) read row `last` (their outputs are
+// masked by the caller).  `x0` is row 0 of the sequence at the first channel, `w8` the 8 channels' weight rows
+// ([8][W], 16 W contiguous bytes).
+template <int W>
+__device__ __forceinline__ void conv_silu8x4(const __bf16* x0, int64_t x_st, int r0, int last, const __bf16* w8,
+                                             const __bf16* st8, uint4 (&out)[4]) {
+  uint32_t w[4 * W];  // packed bf16 pairs: weight (e, j) is bf16 number W e + j
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < W; ++u) {
     const uint4 wu = *reinterpret_cast<const uint4*>(w8 + 8 * u);
     w[4 * u] = wu.x, w[4 * u + 1] = wu.y, w[4 * u + 2] = wu.z, w[4 * u + 3] = wu.w;
   }
@@ -101,16 +103,16 @@ __device__ __forceinline__ void conv4_silu8x4(const __bf16* x0, int64_t x_st, in
     const uint32_t word = w[m >> 1];
     return __uint_as_float((m & 1) ? (word & 0xffff0000u) : (word << 16));
   };
-  uint4 xr[7];
+  uint4 xr[W + 3];
 #pragma unroll
-  for (int m = 0; m < 7; ++m) {
-    const int r = r0 - 3 + m;
+  for (int m = 0; m < W + 3; ++m) {
+    const int r = r0 - (W - 1) + m;
     if (r >= 0) {
       xr[m] = *reinterpret_cast<const uint4*>(x0 + int64_t(min(r, last)) * x_st);
     } else {
       bf16x8 v;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = st8 ? st8[3 * e + 3 + r] : bf(0.f);
+      for (int e = 0; e < 8; ++e) v[e] = st8 ? st8[(W - 1) * e + (W - 1) + r] : bf(0.f);
       xr[m] = __builtin_bit_cast(uint4, v);
     }
   }
@@ -118,11 +120,11 @@ __device__ __forceinline__ void conv4_silu8x4(const __bf16* x0, int64_t x_st, in
   for (int i = 0; i < 4; ++i) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < W; ++j) {
       float xv[8];
       unpack8(xr[i + j], xv);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += wf(4 * e + j) * xv[e];
+      for (int e = 0; e < 8; ++e) acc[e] += wf(W * e + j) * xv[e];
     }
     bf16x8 o;
 #pragma unroll
@@ -132,16 +134,32 @@ __device__ __forceinline__ void conv4_silu8x4(const __bf16* x0, int64_t x_st, in
 }
 
 // The same for one channel (the hot-channel re-fetch), returned as the bf16-rounded value.
-__device__ __forceinline__ float conv4_silu1(const __bf16* x0, int64_t x_st, int t, const __bf16* w4,
-                                            const __bf16* st3) {
+template <int W>
+__device__ __forceinline__ float conv_silu1(const __bf16* x0, int64_t x_st, int t, const __bf16* ww,
+                                           const __bf16* st) {
   float acc = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = t - 3 + j;
-    const float xv = r >= 0 ? f32(x0[int64_t(r) * x_st]) : (st3 ? f32(st3[3 + r]) : 0.f);
-    acc += f32(w4[j]) * xv;
+  for (int j = 0; j < W; ++j) {
+    const int r = t - (W - 1) + j;
+    const float xv = r >= 0 ? f32(x0[int64_t(r) * x_st]) : (st ? f32(st[(W - 1) + r]) : 0.f);
+    acc += f32(ww[j]) * xv;
   }
   return f32(bf(acc / (1.f + __builtin_amdgcn_exp2f(-acc * kLog2e))));
+}
+
+// Calls f(IntC<W>{}) for a convolution width known at run time (2 to 8, uniform over the workgroup; validated by
+// the API): one instantiation of the convolution per width.
+template <typename F>
+__device__ __forceinline__ void with_conv_width(int width, const F& f) {
+  switch (width) {
+    case 2: f(IntC<2>{}); break;
+    case 3: f(IntC<3>{}); break;
+    case 4: f(IntC<4>{}); break;
+    case 5: f(IntC<5>{}); break;
+    case 6: f(IntC<6>{}); break;
+    case 7: f(IntC<7>{}); break;
+    default: f(IntC<8>{}); break;
+  }
 }
 
 // The low-rank gate of the fused prologue for the chunk's 64 rows:
@@ -231,14 +249,17 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
 // ======================================= prep: one workgroup per (chunk, head) =======================================
 // kPro: the fused layer prologue.  0: none (the plain op); 1: `pro.flags` selects the in-kernel q / k
 // normalisation and the beta sigmoid; 2: as 1, and the per-channel gate comes from the low-rank projection; plus 4:
-// the short convolutions of q, k, v run in the kernel too.  Three workgroups fit a CU's LDS; the f16 build, whose
-// diagonal strip tile carries extra bf16 operands, is held to two so that it does not spill.
+// the short convolutions of q, k, v (width 4) run in the kernel too; plus 16 as well: their width is the call's
+// `pro.conv_size` (2 to 8), one code path per width behind a uniform switch.  Three workgroups fit a CU's LDS; the
+// f16 build, whose diagonal strip tile carries extra bf16 operands, and the any-width convolution, whose widest
+// path holds 11 input rows and 8 weight rows per thread, are held to two so that they do not spill.
 template <int VARIANT, int K, int kPro = 0, typename T = __bf16>
-__global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_prep_kernel(const gdr_args a, int nc,
+__global__ __launch_bounds__(256, (__is_same(T, _Float16) || (kPro & 16)) ? 2 : 3) void chunk_prep_kernel(const gdr_args a, int nc,
                                                                                          int64_t rec_bytes,
                                                                                          const gdr_prologue pro) {
   constexpr bool kLowRank = (kPro & 3) == 2;
   constexpr bool kConv = (kPro & 4) != 0;
+  constexpr bool kAnyWidth = (kPro & 16) != 0;  // the convolution's width comes from the call (2 to 8), else 4
   static_assert(!kLowRank || VARIANT == GDR_KDA || VARIANT == GDR_GLA, "low-rank gate: per-channel variants");
   static_assert(kPro == 0 || __is_same(T, __bf16), "the fused prologue reads bf16 inputs");
   using V8 = vec8<T>;
@@ -288,12 +309,28 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
   // fused prologue: in-kernel short convolutions of q, k, v (channels h K + ch of [H K] for q, k; h V + col for v)
   constexpr bool conv = kConv;
   const int64_t ck = int64_t(H) * K, cvv = int64_t(H) * a.value_dim;
-  const __bf16* cwq = static_cast<const __bf16*>(pro.conv_weight[0]) + (int64_t(h) * K) * 4;
-  const __bf16* cwk = static_cast<const __bf16*>(pro.conv_weight[1]) + (int64_t(h) * K) * 4;
-  const __bf16* cwv = static_cast<const __bf16*>(pro.conv_weight[2]) + (int64_t(h) * a.value_dim) * 4;
-  auto state_rows = [&](int i, int64_t nch, int64_t ch0) -> const __bf16* {  // [C][3] rows of this sequence
+  const int cw = kAnyWidth ? pro.conv_size : 4;  // convolution width W
+  const __bf16* cwq = static_cast<const __bf16*>(pro.conv_weight[0]) + (int64_t(h) * K) * cw;
+  const __bf16* cwk = static_cast<const __bf16*>(pro.conv_weight[1]) + (int64_t(h) * K) * cw;
+  const __bf16* cwv = static_cast<const __bf16*>(pro.conv_weight[2]) + (int64_t(h) * a.value_dim) * cw;
+  auto state_rows = [&](int i, int64_t nch, int64_t ch0) -> const __bf16* {  // [C][W - 1] rows of this sequence
     const __bf16* st = static_cast<const __bf16*>(pro.conv_state_in[i]);
-    return st ? st + (int64_t(n) * nch + ch0) * 3 : nullptr;
+    return st ? st + (int64_t(n) * nch + ch0) * (cw - 1) : nullptr;
+  };
+  // 8 channels x 4 rows of the convolution at the call's width
+  auto conv8x4 = [&](const __bf16* x0, int64_t x_st, int r0, const __bf16* w8, const __bf16* st8, uint4 (&o)[4]) {
+    if constexpr (kAnyWidth)
+      with_conv_width(cw, [&](auto wc) { conv_silu8x4<decltype(wc)::value>(x0, x_st, r0, len - 1, w8, st8, o); });
+    else
+      conv_silu8x4<4>(x0, x_st, r0, len - 1, w8, st8, o);
+  };
+  auto conv1 = [&](const __bf16* x0, int64_t x_st, int t, const __bf16* ww, const __bf16* st) {
+    float r = 0.f;
+    if constexpr (kAnyWidth)
+      with_conv_width(cw, [&](auto wc) { r = conv_silu1<decltype(wc)::value>(x0, x_st, t, ww, st); });
+    else
+      r = conv_silu1<4>(x0, x_st, t, ww, st);
+    return r;
   };
 
   T* kap = reinterpret_cast<T*>(smem + L::KAP);
@@ -333,7 +370,7 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
     if constexpr (kConv) {
       const int u = min(int(threadIdx.x), 16 * w8 - 1);
       const int col = pass * K + (u % w8) * 8;
-      conv4_silu8x4(x.vp + col, x.v_st, c * kChunk + 4 * (u / w8), len - 1, cwv + col * 4,
+      conv8x4(x.vp + col, x.v_st, c * kChunk + 4 * (u / w8), cwv + col * cw,
                     state_rows(2, cvv, int64_t(h) * a.value_dim + col), vpre);
     } else {
 #pragma unroll
@@ -406,8 +443,8 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
       if (u < kUnits) {
         const int tsr = u / (16 * G8), rq = (u / G8) % 16, ch = (u % G8) * 8;
         uint4 o[4];
-        conv4_silu8x4((tsr ? x.kp : x.qp) + ch, tsr ? x.k_st : x.q_st, c * kChunk + 4 * rq, len - 1,
-                      (tsr ? cwk : cwq) + ch * 4, state_rows(tsr, ck, int64_t(h) * K + ch), o);
+        conv8x4((tsr ? x.kp : x.qp) + ch, tsr ? x.k_st : x.q_st, c * kChunk + 4 * rq, (tsr ? cwk : cwq) + ch * cw,
+                state_rows(tsr, ck, int64_t(h) * K + ch), o);
         T* tile = tsr ? kd : kap;
 #pragma unroll
         for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(tile + (4 * rq + i) * KP + ch) = o[i];
@@ -670,8 +707,8 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
         auto rows = [&](int tcr, int ch, float& q, float& k, float& g) {
           InputRowsT<T>{x, kGate}(tcr, ch, q, k, g);  // g is replaced below when it is computed
           if (conv) {
-            q = conv4_silu1(x.qp + ch, x.q_st, tcr, cwq + ch * 4, state_rows(0, ck, int64_t(h) * K + ch));
-            k = conv4_silu1(x.kp + ch, x.k_st, tcr, cwk + ch * 4, state_rows(1, ck, int64_t(h) * K + ch));
+            q = conv1(x.qp + ch, x.q_st, tcr, cwq + ch * cw, state_rows(0, ck, int64_t(h) * K + ch));
+            k = conv1(x.kp + ch, x.k_st, tcr, cwk + ch * cw, state_rows(1, ck, int64_t(h) * K + ch));
           }
           const int r = tcr - c * kChunk;          // row within the chunk (clamped rows stay inside it)
           if (norm) q = f32(cv<T>(q * snorm[r])), k = f32(cv<T>(k * snorm[64 + r]));
@@ -824,19 +861,19 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
     }
   }
 
-  // fused prologue: the last chunk of a sequence stores the last 3 inputs of each of its head's q, k, v channels,
-  // reaching back into the state it was given when the sequence is shorter than 3
+  // fused prologue: the last chunk of a sequence stores the last W - 1 inputs of each of its head's q, k, v
+  // channels, reaching back into the state it was given when the sequence is shorter than W - 1
   if constexpr (kConv) {
   if ((c + 1) * kChunk >= len) {
-    const int V = a.value_dim, nqk = 2 * K * 3, ntot = nqk + V * 3;
+    const int S = cw - 1, V = a.value_dim, nqk = 2 * K * S, ntot = nqk + V * S;
     for (int idx = threadIdx.x; idx < ntot; idx += 256) {
-      const int i = idx < nqk ? idx / (K * 3) : 2;
-      const int rem = idx < nqk ? idx % (K * 3) : idx - nqk, ch = rem / 3, sl = rem % 3;
+      const int i = idx < nqk ? idx / (K * S) : 2;
+      const int rem = idx < nqk ? idx % (K * S) : idx - nqk, ch = rem / S, sl = rem % S;
       __bf16* so = static_cast<__bf16*>(pro.conv_state_out[i]);
       if (!so) continue;
       const int64_t nch = i < 2 ? ck : cvv;
       const int64_t row = int64_t(n) * nch + (i < 2 ? int64_t(h) * K : int64_t(h) * V) + ch;
-      const int r = len - 3 + sl;
+      const int r = len - S + sl;
       __bf16 val;
       if (r >= 0) {
         const __bf16* xp = i == 0 ? x.qp : i == 1 ? x.kp : x.vp;
@@ -844,9 +881,9 @@ __global__ __launch_bounds__(256, __is_same(T, _Float16) ? 2 : 3) void chunk_pre
         val = xp[int64_t(r) * xs + ch];
       } else {
         const __bf16* si = static_cast<const __bf16*>(pro.conv_state_in[i]);
-        val = si ? si[row * 3 + sl + len] : bf(0.f);
+        val = si ? si[row * S + sl + len] : bf(0.f);
       }
-      so[row * 3 + sl] = val;
+      so[row * S + sl] = val;
     }
   }
   }
@@ -1279,15 +1316,19 @@ hipError_t launch_split_typed(const gdr_args& a, const gdr_prologue& pro, hipStr
   }
   hipError_t e;
   const bool conv = pro.flags & GDR_PRO_CONV;
+  const bool any_width = conv && pro.conv_size != 4;  // widths other than 4: one kernel per mode for all of them
   if (!pro.flags) {
     e = launch_prep<VARIANT, K, 0>(a, pro, stream);
   } else if constexpr (VARIANT == GDR_KDA || VARIANT == GDR_GLA) {
     if (pro.flags & GDR_PRO_GATE_LOWRANK)
-      e = conv ? launch_prep<VARIANT, K, 6>(a, pro, stream) : launch_prep<VARIANT, K, 2>(a, pro, stream);
+      e = !conv ? launch_prep<VARIANT, K, 2>(a, pro, stream)
+                : any_width ? launch_prep<VARIANT, K, 22>(a, pro, stream) : launch_prep<VARIANT, K, 6>(a, pro, stream);
     else
-      e = conv ? launch_prep<VARIANT, K, 5>(a, pro, stream) : launch_prep<VARIANT, K, 1>(a, pro, stream);
+      e = !conv ? launch_prep<VARIANT, K, 1>(a, pro, stream)
+                : any_width ? launch_prep<VARIANT, K, 21>(a, pro, stream) : launch_prep<VARIANT, K, 5>(a, pro, stream);
   } else {
-    e = conv ? launch_prep<VARIANT, K, 5>(a, pro, stream) : launch_prep<VARIANT, K, 1>(a, pro, stream);
+    e = !conv ? launch_prep<VARIANT, K, 1>(a, pro, stream)
+              : any_width ? launch_prep<VARIANT, K, 21>(a, pro, stream) : launch_prep<VARIANT, K, 5>(a, pro, stream);
   }
   if (e != hipSuccess) return e;
   return launch_scan<VARIANT, K, OutT, kScanOut>(a, nullptr, nullptr, stream);

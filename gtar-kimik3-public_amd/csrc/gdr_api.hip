@@ -122,9 +122,8 @@ int check_prologue(const gdr_args* a, const gdr_prologue* pro) {
   if ((pro->flags & GDR_PRO_BETA_LOGITS) && a->variant == GDR_GLA)
     return fail(GDR_ERR_INVALID, "GLA takes no beta (GDR_PRO_BETA_LOGITS)");
   if (pro->flags & GDR_PRO_CONV) {
-    if (pro->conv_size != 4)
-      return fail(GDR_ERR_UNSUPPORTED, "in-kernel convolution of width %d not supported (4; gdr_short_conv_fwd takes "
-                  "2 to 8)", pro->conv_size);
+    if (pro->conv_size < 2 || pro->conv_size > 8)
+      return fail(GDR_ERR_UNSUPPORTED, "in-kernel convolution of width %d not supported (2 to 8)", pro->conv_size);
     const char* names[] = {"q", "k", "v"};
     for (int i = 0; i < 3; ++i) {
       if (!pro->conv_weight[i] || reinterpret_cast<uintptr_t>(pro->conv_weight[i]) % 16)

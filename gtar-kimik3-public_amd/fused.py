@@ -11,7 +11,8 @@ and head at K = 128), written by the layer and read back by the op.  Here the op
 z = decay_proj[0](x) instead (R bf16 values per token, shared by all heads), together with decay_proj[1]'s weight
 and bias and A_log, and computes the gate inside the kernel on MFMA; it also normalises q and k and applies the
 beta sigmoid there.  With `conv_weights`, q, k and v are the short convolutions' inputs (q_proj(x), k_proj(x),
-v_proj(x)) and the kernel also applies the three depthwise convolutions of width 4 and their SiLU
+v_proj(x)) and the kernel also applies the three depthwise convolutions (any width from 2 to 8, 4 in the layer)
+and their SiLU
 (ShortConvolution, src/layers/short_convolution.py:11-20), reading each sequence's conv state and, like the
 reference's cache path (:16-19), updating it in place.  Gradients are not provided: training keeps the unfused op,
 which is differentiable.
@@ -97,20 +98,24 @@ def _fused(variant, query, key, value, gate_lowrank, gate_weight, gate_bias, a_l
         if len(conv_weights) != 3:
             raise ValueError(f"{name}: conv_weights must hold the q, k and v convolution weights")
         channels = (heads * key_dim, heads * key_dim, heads * value_dim)
+        width = conv_weights[0].shape[-1]
+        if not 2 <= width <= 8:
+            raise NotImplementedError(f"{name}: in-kernel convolution of width {width}; widths 2 to 8 are supported")
         conv_w = []
         for wt, ch, nm in zip(conv_weights, channels, "qkv"):
             wt = wt.reshape(wt.shape[0], -1) if wt.dim() == 3 else wt
-            if tuple(wt.shape) != (ch, 4):
-                raise ValueError(f"{name}: {nm} conv weight must be [{ch}, 4] (or [{ch}, 1, 4]): the in-kernel "
-                                 f"convolution has width 4; got {tuple(conv_weights[len(conv_w)].shape)}")
+            if tuple(wt.shape) != (ch, width):
+                raise ValueError(f"{name}: {nm} conv weight must be [{ch}, {width}] (or [{ch}, 1, {width}]), one width "
+                                 f"for q, k and v; got {tuple(conv_weights[len(conv_w)].shape)}")
             conv_w.append(_aligned16(wt.to(torch.bfloat16).contiguous()))
         if conv_states is not None:
             if len(conv_states) != 3:
                 raise ValueError(f"{name}: conv_states must hold the q, k and v conv states")
             states_in = []
             for st, ch, nm in zip(conv_states, channels, "qkv"):
-                if tuple(st.shape) != (n_states, ch, 3):
-                    raise ValueError(f"{name}: {nm} conv state must be [{n_states}, {ch}, 3], got {tuple(st.shape)}")
+                if tuple(st.shape) != (n_states, ch, width - 1):
+                    raise ValueError(f"{name}: {nm} conv state must be [{n_states}, {ch}, {width - 1}], got "
+                                     f"{tuple(st.shape)}")
                 states_in.append(st.to(torch.bfloat16).contiguous())
             states_out = [st.clone() for st in states_in]  # a sequence of length 0 keeps its state
 

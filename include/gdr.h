@@ -107,7 +107,7 @@ int gdr_chunk_fwd(const gdr_args* args, hipStream_t stream);
                                   from the rank-R activations z of the gate's first projection; args->gate must
                                   be NULL */
 #define GDR_PRO_CONV 8         /* q, k, v are the short convolutions' inputs (q_proj(x), k_proj(x), v_proj(x)): the
-                                  kernel applies each depthwise causal convolution of width 4 and the SiLU
+                                  kernel applies each depthwise causal convolution (width conv_size) and the SiLU
                                   (ShortConvolution, src/layers/short_convolution.py:11-20) before the
                                   normalisation, with each sequence's conv state */
 typedef struct gdr_prologue {
@@ -117,7 +117,7 @@ typedef struct gdr_prologue {
   const void* gate_weight;  /* [H * K, R] bf16 row-major, 16-byte aligned: decay_proj[1].weight */
   const float* gate_bias;   /* [H * K] f32, 16-byte aligned, or NULL: decay_proj[1].bias */
   const float* a_log;       /* [H] f32: A_log */
-  int32_t conv_size;        /* CONV: the convolutions' width W; must be 4 */
+  int32_t conv_size;        /* CONV: the convolutions' width W, 2 to 8 (4, the layer's default, has its own build) */
   int32_t conv_reserved;
   const void* conv_weight[3];    /* CONV: q, k, v weights [H * D, W] bf16 (nn.Conv1d weight [C, 1, W]), 16-byte
                                     aligned; D = K for q, k and V for v */

@@ -256,10 +256,13 @@ def test_fused_prologue_rejects_bad_arguments_without_a_gpu():
     assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -1
     assert b"flags" in so.gdr_last_error()
     pro.flags = lib.PRO_CONV
-    pro.conv_size = 3  # the in-kernel convolution has width 4
+    pro.conv_size = 9  # the in-kernel convolution takes widths 2 to 8
     assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -2
-    assert b"width 3" in so.gdr_last_error()
-    pro.conv_size = 4
+    assert b"width 9" in so.gdr_last_error()
+    pro.conv_size = 1
+    assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -2
+    assert b"width 1" in so.gdr_last_error()
+    pro.conv_size = 3
     pro.conv_weight[0], pro.conv_weight[1] = 4096, 8192  # v's weight missing
     assert so.gdr_chunk_fwd_fused(ctypes.byref(args), ctypes.byref(pro), None) == -1
     assert b"conv_weight[2]" in so.gdr_last_error()

@@ -6,7 +6,7 @@ Convolution parity: against the oracle's `short_convolution` (pinned against nn.
 relative Frobenius error <= 1e-2); the oracle sees the convolution outputs rounded to bf16, as the kernel (and the
 reference's bf16 layer) rounds them.  The updated conv states are copies of inputs, so they are compared exactly, and
 the fused call must equal, bit for bit, gdr_short_conv_fwd followed by the fused op without the convolution (both
-accumulate the four taps in the same order and round once).
+accumulate the W taps in the same order and round once), for the layer's width 4 and the other widths 2 to 8.
 
 Epilogue parity: against the layer's own expression evaluated by PyTorch on the same device
 (`weight * (x.float() * rsqrt(mean(x^2) + eps)).to(x.dtype) * F.silu(gate)`), to one rounding of the output dtype,
@@ -24,14 +24,14 @@ from _helpers import OUT_TOL, STATE_TOL, gdr, oracle, out_error, state_error
 pytestmark = pytest.mark.gpu
 
 
-def _inputs(B, T, H, K, V, R, seed, n_states):
+def _inputs(B, T, H, K, V, R, seed, n_states, width=4):
     gen = torch.Generator().manual_seed(seed)
     xq = (torch.randn(B, T, H * K, generator=gen) * 2.0).bfloat16()
     xk = (torch.randn(B, T, H * K, generator=gen) * 2.0).bfloat16()
     xv = torch.randn(B, T, H * V, generator=gen).bfloat16()
-    bound = 1 / math.sqrt(4)
-    cw = [((torch.rand(c, 1, 4, generator=gen) * 2 - 1) * bound).bfloat16() for c in (H * K, H * K, H * V)]
-    cs = [torch.randn(n_states, c, 3, generator=gen).bfloat16() for c in (H * K, H * K, H * V)]
+    bound = 1 / math.sqrt(width)
+    cw = [((torch.rand(c, 1, width, generator=gen) * 2 - 1) * bound).bfloat16() for c in (H * K, H * K, H * V)]
+    cs = [torch.randn(n_states, c, width - 1, generator=gen).bfloat16() for c in (H * K, H * K, H * V)]
     z = torch.randn(B, T, R, generator=gen).bfloat16()
     w = (torch.randn(H * K, R, generator=gen) / math.sqrt(R)).bfloat16()
     dt = torch.exp(torch.empty(H * K).uniform_(math.log(1e-3), math.log(1e-1), generator=gen))
@@ -70,11 +70,12 @@ def _run(H, xq, xk, xv, cw, cs, z, w, bias, a_log, logits, h0, cu=None, with_sta
     return out, fs, states
 
 
+@pytest.mark.parametrize("width", [4, 2, 3, 8])
 @pytest.mark.parametrize("shape", [(2, 200, 2, 128, 128, 128), (1, 130, 3, 64, 64, 32), (1, 3, 2, 128, 128, 64)])
-def test_fused_conv_matches_oracle(shape):
+def test_fused_conv_matches_oracle(shape, width):
     B, T, H, K, V, R = shape
-    print(f"fused conv kda B={B} T={T} H={H} K={K} V={V} R={R}", flush=True)
-    xq, xk, xv, cw, cs, z, w, bias, a_log, logits, h0 = _inputs(B, T, H, K, V, R, seed=1, n_states=B)
+    print(f"fused conv kda B={B} T={T} H={H} K={K} V={V} R={R} W={width}", flush=True)
+    xq, xk, xv, cw, cs, z, w, bias, a_log, logits, h0 = _inputs(B, T, H, K, V, R, seed=1, n_states=B, width=width)
     out, fs, states = _run(H, xq, xk, xv, cw, cs, z, w, bias, a_log, logits, h0)
     ref_o, ref_s, ref_cs = _oracle(H, xq, xk, xv, cw, cs, z, w, bias, a_log, logits, h0)
     eo, es = out_error(out, ref_o), state_error(fs, ref_s)
@@ -84,14 +85,15 @@ def test_fused_conv_matches_oracle(shape):
         assert torch.equal(got.cpu(), want)
 
 
-def test_fused_conv_packed_sequences():
-    """cu_seqlens: every sequence starts its convolutions from its own state (lengths around the 3-row halo and the
-    64-row chunk edges, and a sequence shorter than the state)."""
-    lens = [1, 2, 3, 4, 63, 64, 65, 130]
+@pytest.mark.parametrize("width", [4, 2, 6, 8])
+def test_fused_conv_packed_sequences(width):
+    """cu_seqlens: every sequence starts its convolutions from its own state (lengths around the W - 1-row halo and
+    the 64-row chunk edges, and sequences shorter than the state)."""
+    lens = [1, 2, 3, 4, 5, 7, 63, 64, 65, 130]
     cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
     H, K, V, R = 2, 128, 128, 64
     xq, xk, xv, cw, cs, z, w, bias, a_log, logits, h0 = _inputs(1, int(cu[-1]), H, K, V, R, seed=3,
-                                                                  n_states=len(lens))
+                                                                  n_states=len(lens), width=width)
     out, fs, states = _run(H, xq, xk, xv, cw, cs, z, w, bias, a_log, logits, h0, cu=cu)
     ref_o, ref_s, ref_cs = _oracle(H, xq, xk, xv, cw, cs, z, w, bias, a_log, logits, h0, cu=cu)
     eo, es = out_error(out, ref_o), state_error(fs, ref_s)
@@ -101,11 +103,12 @@ def test_fused_conv_packed_sequences():
         assert torch.equal(got.cpu(), want)
 
 
-def test_fused_conv_equals_separate_convolutions():
+@pytest.mark.parametrize("width", [4, 3, 8])
+def test_fused_conv_equals_separate_convolutions(width):
     """Bit-identical to gdr_short_conv_fwd on q, k, v followed by the fused op without the convolution, with and
     without conv states (zero history)."""
     B, T, H, K, V, R = 2, 300, 4, 128, 128, 128
-    xq, xk, xv, cw, cs, z, w, bias, a_log, logits, h0 = _inputs(B, T, H, K, V, R, seed=4, n_states=B)
+    xq, xk, xv, cw, cs, z, w, bias, a_log, logits, h0 = _inputs(B, T, H, K, V, R, seed=4, n_states=B, width=width)
     for with_states in (True, False):
         out, fs, _ = _run(H, xq, xk, xv, cw, cs, z, w, bias, a_log, logits, h0, with_states=with_states)
         with torch.no_grad():
