@@ -170,10 +170,34 @@ __device__ __forceinline__ void with_conv_width(int width, const F& f) {
 // chunk c ^ (r mod K / 8), copied with global_load_lds_dwordx4: the permutation is applied to the source addresses,
 // since the copy lands lane i at base + 16 i).  Lane (l16, g4) ends with channels 16 t + 4 g4 + i of token 16 j + l16;
 // the values go to the fp32 LDS rows `gst` (row pitch K + 4), from which every lane later reads its own row.
-// `after_first_block()` runs once the first block of z and W has arrived, before its products: the caller issues its
-// own row loads there, so that their latency overlaps the gate's products instead of following them (the
-// barriers below order LDS only and do not wait for those loads).
-template <int K, typename AfterFirstBlock>
+// s_waitcnt vmcnt(N) and the workgroup barrier, tied to the low-rank gate's W fragments and bias (loaded by inline
+// assembly, so the compiler does not track them): no instruction reading them can be scheduled before the wait.
+template <int N, int CT, int S>
+__device__ __forceinline__ void wait_tied(bf16x8 (&wa)[CT][S], floatx4 (&bias)[CT]) {
+  static_assert(CT * S == 8 || CT * S == 2, "every W fragment is tied");
+  if constexpr (CT * S == 8)
+    asm volatile("s_waitcnt vmcnt(%10)\n\ts_barrier"
+                 : "+v"(wa[0][0]), "+v"(wa[0][1]), "+v"(wa[0][2]), "+v"(wa[0][3]), "+v"(wa[CT - 1][0]),
+                   "+v"(wa[CT - 1][1]), "+v"(wa[CT - 1][2]), "+v"(wa[CT - 1][3]), "+v"(bias[0]), "+v"(bias[CT - 1])
+                 : "n"(N)
+                 : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(%3)\n\ts_barrier"
+                 : "+v"(wa[0][0]), "+v"(wa[0][S - 1]), "+v"(bias[0])
+                 : "n"(N)
+                 : "memory");
+}
+
+// `after_first_block()` issues the caller's own row loads (kAfterLoads vector loads per lane) right behind the first
+// block's W and z requests.  One counted wait, vmcnt(kAfterLoads), then lets the block's products start while those
+// row loads are still in flight, so their latency overlaps the gate instead of following it.  For that count to hold:
+//   * the W fragments and the bias are loaded by inline assembly, and the z fragments are read from LDS by inline
+//     assembly: the compiler does not see them as loads, so it does not put a wait of its own (a vmcnt(0) behind the
+//     z copies, whose LDS writes it cannot tell apart from these reads) in front of the products;
+//   * the counted wait is tied ("+v") to every W fragment and bias register, so no instruction reading them can be
+//     scheduled before it, and it carries the workgroup barrier after which every wave's z copies have landed;
+//   * scheduling barriers keep the row loads behind the copies (vector memory requests complete in issue order).
+template <int K, int kAfterLoads, typename AfterFirstBlock>
 __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h, const __bf16* zchunk, int64_t z_st,
                                                   int last_row, float* gst, __bf16* zs, int wave, int l16, int g4,
                                                   const AfterFirstBlock& after_first_block) {
@@ -189,11 +213,12 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
   // A_log and the bias are requested first, and each block's W fragments before its z rows: one wait then covers
   // every load of a block, instead of a memory round trip per dependent fragment.
   const float a_log_h = pro.a_log[h];
-  float4 bias[CT];
+  floatx4 bias[CT];
+  const float* bias_p = pro.gate_bias ? pro.gate_bias + size_t(h) * K + ch0 + 4 * g4 : nullptr;
 #pragma unroll
   for (int t = 0; t < CT; ++t) {
-    bias[t] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (pro.gate_bias) bias[t] = *reinterpret_cast<const float4*>(pro.gate_bias + size_t(h) * K + ch0 + 16 * t + 4 * g4);
+    bias[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (bias_p) asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(bias[t]) : "v"(bias_p + 16 * t));
   }
   for (int r0 = 0; r0 < R; r0 += RB) {  // the accumulators start at zero right before this loop
     bf16x8 wa[CT][RB / 32];
@@ -201,8 +226,10 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
     for (int t = 0; t < CT; ++t)
 #pragma unroll
       for (int s = 0; s < RB / 32; ++s)
-        wa[t][s] = *reinterpret_cast<const bf16x8*>(w + size_t(16 * t) * R + min(r0 + 32 * s, R - 32));
-    // stage z[0:64][r0 : r0 + RB] (columns past R read column R - 8 and meet zero W operands below)
+        asm volatile("global_load_dwordx4 %0, %1, off"
+                     : "=v"(wa[t][s])
+                     : "v"(w + size_t(16 * t) * R + min(r0 + 32 * s, R - 32)));
+    // stage z[0:64][r0 : r0 + RB] (columns past R read column R - 8 and meet zero z operands below)
 #pragma unroll
     for (int k = 0; k < 64 * C16 / 256; ++k) {
       const int slot = 64 * (4 * k + wave) + lane;  // LDS chunk index: row slot / C16, chunk slot % C16
@@ -210,24 +237,37 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
       const int col = min(r0 + 8 * c, R - 8);
       lds_dma16(zchunk + int64_t(min(row, last_row)) * z_st + col, zs + 8 * 64 * (4 * k + wave));
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    lds_barrier();
-    if (r0 == 0) after_first_block();
+    // Wait for this block's W, bias and z (the caller's row loads, issued after them, may stay in flight), then
+    // the barrier: every wave's z copies have landed.
+    if (r0 == 0) {
+      __builtin_amdgcn_sched_barrier(0);
+      after_first_block();
+      __builtin_amdgcn_sched_barrier(0);
+      wait_tied<kAfterLoads>(wa, bias);
+    } else {
+      wait_tied<0>(wa, bias);
+    }
 #pragma unroll
     for (int s = 0; s < RB / 32; ++s) {
       const bool live = r0 + 32 * s < R;
-      bf16x8 zb[4];
+      bf16x8 zb[4];  // rows 16 j + l16 of zs, columns r0 + 32 s + 8 g4 .. + 7 (the four rows share the swizzle)
+      const int c = (4 * s + g4) ^ (l16 % C16);
+      const uint32_t za = static_cast<uint32_t>(
+          (uintptr_t)(__attribute__((address_space(3))) const __bf16*)(zs + l16 * RB + 8 * c));
+      asm volatile(
+          "ds_read_b128 %0, %4\n\t"
+          "ds_read_b128 %1, %4 offset:%5\n\t"
+          "ds_read_b128 %2, %4 offset:%6\n\t"
+          "ds_read_b128 %3, %4 offset:%7\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(zb[0]), "=&v"(zb[1]), "=&v"(zb[2]), "=&v"(zb[3])
+          : "v"(za), "n"(2 * 16 * RB), "n"(2 * 32 * RB), "n"(2 * 48 * RB));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = 16 * j + l16, c = (4 * s + g4) ^ (row % C16);
-        zb[j] = *reinterpret_cast<const bf16x8*>(zs + row * RB + 8 * c);
-      }
+      for (int j = 0; j < 4; ++j) zb[j] = live ? zb[j] : bf16x8{};
 #pragma unroll
-      for (int t = 0; t < CT; ++t) {
-        const bf16x8 wf = live ? wa[t][s] : bf16x8{};
+      for (int t = 0; t < CT; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[t][j] = mfma32(wf, zb[j], acc[t][j]);
-      }
+        for (int j = 0; j < 4; ++j) acc[t][j] = mfma32(wa[t][s], zb[j], acc[t][j]);
     }
     lds_barrier();  // every wave is done with this block of zs
   }
@@ -235,7 +275,7 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
 #pragma unroll
   for (int t = 0; t < CT; ++t) {
     const int ch = ch0 + 16 * t + 4 * g4;
-    const float4 bias_t = bias[t];
+    const float4 bias_t = make_float4(bias[t][0], bias[t][1], bias[t][2], bias[t][3]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float4 g = make_float4(
@@ -405,7 +445,7 @@ __global__ __launch_bounds__(256, (__is_same(T, _Float16) || (kPro & 16)) ? 2 : 
     // The gate rows are computed into the KAP / KD region, which nothing uses before step 3b (after two barriers).
     const __bf16* zchunk = static_cast<const __bf16*>(pro.gate_lowrank.ptr) + bidx * pro.gate_lowrank.stride_b +
                            int64_t(bos + c * kChunk) * pro.gate_lowrank.stride_t;
-    auto issue_rows = [&]() {  // without the in-kernel convolution: this lane's q, k rows and the first V pass
+    auto issue_rows = [&]() {  // without the in-kernel convolution: this lane's q, k rows (kAfterLoads = 2 KS loads)
       if constexpr (!kConv) {
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) {
@@ -413,10 +453,9 @@ __global__ __launch_bounds__(256, (__is_same(T, _Float16) || (kPro & 16)) ? 2 : 
           qraw[kk] = *reinterpret_cast<const uint4*>(x.qp + tc * x.q_st + ch);
           kraw[kk] = *reinterpret_cast<const uint4*>(x.kp + tc * x.k_st + ch);
         }
-        load_v_pass(0);
       }
     };
-    lowrank_gate_rows<K>(pro, h, zchunk, pro.gate_lowrank.stride_t, len - 1 - c * kChunk,
+    lowrank_gate_rows<K, kConv ? 0 : 2 * KS>(pro, h, zchunk, pro.gate_lowrank.stride_t, len - 1 - c * kChunk,
                          reinterpret_cast<float*>(smem), reinterpret_cast<__bf16*>(smem + L::SC), wave, l16, g4,
                          issue_rows);
     lds_barrier();
@@ -521,7 +560,7 @@ __global__ __launch_bounds__(256, (__is_same(T, _Float16) || (kPro & 16)) ? 2 : 
       kraw[kk] = *reinterpret_cast<const uint4*>(&nk);
     }
   }
-  if constexpr (!kLowRank || kConv) load_v_pass(0);
+  load_v_pass(0);
 
   // ---- 2. in-block inclusive cumsum of the log2 gate over the 16 rows (one DPP row per channel group) ----
   if constexpr (kGate) {

@@ -49,7 +49,8 @@ def _cuda(*xs):
     return [None if x is None else x.cuda() for x in xs]
 
 
-@pytest.mark.parametrize("shape", [(2, 200, 2, 128, 128, 128), (1, 130, 3, 64, 64, 32), (1, 64, 2, 128, 256, 256)])
+@pytest.mark.parametrize("shape", [(2, 200, 2, 128, 128, 128), (1, 130, 3, 64, 64, 32), (1, 64, 2, 128, 256, 256),
+                                   (1, 130, 3, 64, 64, 192), (1, 100, 2, 128, 128, 96)])
 def test_fused_kda_matches_oracle(shape):
     B, T, H, K, V, R = shape
     print(f"fused kda B={B} T={T} H={H} K={K} V={V} R={R}", flush=True)
