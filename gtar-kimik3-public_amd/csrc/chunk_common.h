@@ -82,6 +82,35 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
 
+// Non-temporal (`nt`) 16-byte accesses.  The prefill's records, written by the prep and read back by the scan,
+// come from the memory-side cache when they are still in it; for calls where that pays, input rows that no other
+// workgroup reads and outputs that the call does not read back are loaded and stored with the hint, so that they
+// do not displace the records.  `load_nt16` is a global load whose form is fixed at compile time (the kernels that
+// use it are instantiated with and without the hint: two global loads of one address that differ only in the hint
+// would be merged into one plain load).  `store_nt16` is a raw buffer store with the `nt` cache-policy bit, a
+// different instruction from the plain global store, so a kernel can choose between the two at run time; its
+// base is wave-uniform and the byte offset must satisfy off + 16 <= 2^32.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <typename R>
+__device__ __forceinline__ R load_nt16(const void* p) {
+  static_assert(sizeof(R) == 16, "16-byte vector");
+  return __builtin_bit_cast(R, __builtin_nontemporal_load(static_cast<const u32x4*>(p)));
+}
+template <typename V>
+__device__ __forceinline__ void store_nt16(void* base, uint32_t off, const V& v) {
+  static_assert(sizeof(V) == 16, "16-byte vector");
+  constexpr int kCachePolicyNT = 2;  // the `nt` bit of a buffer access's cache-policy operand
+  // raw buffer (stride 0) over the 4 GiB from base, held in scalar registers (base is wave-uniform); third dword
+  // 0x00020000: the 32-bit data format gfx9 expects
+  // (readfirstlane returns a signed int: each half goes through uint32_t so that it is zero-extended)
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(b))));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(b >> 32))));
+  void* ub = reinterpret_cast<void*>(uint64_t(lo) | (uint64_t(hi) << 32));
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(ub, 0, -1, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rsrc, off, 0, kCachePolicyNT);
+}
+
 // Workgroup barrier that orders LDS only: global stores issued before it are not waited for (a full
 // __syncthreads() also drains outstanding global memory operations).
 __device__ __forceinline__ void lds_barrier() {

@@ -28,7 +28,9 @@
 // 16x16 blocks of (I + diag(beta) P) are inverted in fp32; W and U come out of a blocked forward substitution on
 // v_mfma_f32_16x16x16_bf16 with fp32 accumulation.  W, U, Q e^B and K e^{B_end - B} are stored as bf16, as the
 // reference stores W, U and u.
+#include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "chunk_common.h"
 #include "gdr_internal.h"
@@ -287,13 +289,21 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
 }
 
 // ======================================= prep: one workgroup per (chunk, head) =======================================
+// 16 bytes of an input row that only this workgroup reads: with the non-temporal hint when kNT.
+template <bool kNT, typename R>
+__device__ __forceinline__ R input16(const void* p) {
+  if constexpr (kNT) return load_nt16<R>(p);
+  else return *static_cast<const R*>(p);
+}
+
 // kPro: the fused layer prologue.  0: none (the plain op); 1: `pro.flags` selects the in-kernel q / k
 // normalisation and the beta sigmoid; 2: as 1, and the per-channel gate comes from the low-rank projection; plus 4:
 // the short convolutions of q, k, v (width 4) run in the kernel too; plus 16 as well: their width is the call's
 // `pro.conv_size` (2 to 8), one code path per width behind a uniform switch.  Three workgroups fit a CU's LDS; the
 // f16 build, whose diagonal strip tile carries extra bf16 operands, and the any-width convolution, whose widest
-// path holds 11 input rows and 8 weight rows per thread, are held to two so that they do not spill.
-template <int VARIANT, int K, int kPro = 0, typename T = __bf16>
+// path holds 11 input rows and 8 weight rows per thread, are held to two so that they do not spill.  kNT (plain
+// op only): the q, k, gate and V rows are loaded with the non-temporal hint (`use_nt_hint` below decides).
+template <int VARIANT, int K, int kPro = 0, typename T = __bf16, bool kNT = false>
 __global__ __launch_bounds__(256, (__is_same(T, _Float16) || (kPro & 16)) ? 2 : 3) void chunk_prep_kernel(const gdr_args a, int nc,
                                                                                          int64_t rec_bytes,
                                                                                          const gdr_prologue pro) {
@@ -418,7 +428,7 @@ __global__ __launch_bounds__(256, (__is_same(T, _Float16) || (kPro & 16)) ? 2 : 
         const int pc = min(int(threadIdx.x) + 256 * i, 64 * w8 - 1);
         const int row = pc / w8, cc = (pc % w8) * 8;
         const int t = min(c * kChunk + row, len - 1);
-        vpre[i] = *reinterpret_cast<const uint4*>(x.vp + t * x.v_st + pass * K + cc);
+        vpre[i] = input16<kNT, uint4>(x.vp + t * x.v_st + pass * K + cc);
       }
     }
   };
@@ -498,8 +508,8 @@ __global__ __launch_bounds__(256, (__is_same(T, _Float16) || (kPro & 16)) ? 2 : 
       qraw[kk] = *reinterpret_cast<const uint4*>(kap + (16 * p + l16) * KP + ch);
       kraw[kk] = *reinterpret_cast<const uint4*>(kd + (16 * p + l16) * KP + ch);
     } else if constexpr (!kLowRank) {  // (with the low-rank gate they were requested during its products)
-      qraw[kk] = *reinterpret_cast<const uint4*>(x.qp + tc * x.q_st + ch);
-      kraw[kk] = *reinterpret_cast<const uint4*>(x.kp + tc * x.k_st + ch);
+      qraw[kk] = input16<kNT, uint4>(x.qp + tc * x.q_st + ch);
+      kraw[kk] = input16<kNT, uint4>(x.kp + tc * x.k_st + ch);
     }
     if constexpr (kLowRank && kConv) {
       // bl was read before the conv stage
@@ -510,8 +520,8 @@ __global__ __launch_bounds__(256, (__is_same(T, _Float16) || (kPro & 16)) ? 2 : 
       bl[kk][0] = g0.x; bl[kk][1] = g0.y; bl[kk][2] = g0.z; bl[kk][3] = g0.w;
       bl[kk][4] = g1.x; bl[kk][5] = g1.y; bl[kk][6] = g1.z; bl[kk][7] = g1.w;
     } else if constexpr (kGate == 2) {
-      const float4 g0 = *reinterpret_cast<const float4*>(x.gp + tc * x.g_st + ch);
-      const float4 g1 = *reinterpret_cast<const float4*>(x.gp + tc * x.g_st + ch + 4);
+      const float4 g0 = input16<kNT, float4>(x.gp + tc * x.g_st + ch);
+      const float4 g1 = input16<kNT, float4>(x.gp + tc * x.g_st + ch + 4);
       bl[kk][0] = g0.x; bl[kk][1] = g0.y; bl[kk][2] = g0.z; bl[kk][3] = g0.w;
       bl[kk][4] = g1.x; bl[kk][5] = g1.y; bl[kk][6] = g1.z; bl[kk][7] = g1.w;
     }
@@ -949,7 +959,7 @@ struct ScanShape {
 template <int VARIANT, int K, typename OutT, int SL, int NT, int kMode = kScanOut, typename T = __bf16>
 __global__ __launch_bounds__((ScanShape<SL, NT>::threads(kMode)), 1) void chunk_scan_kernel(const gdr_args a, int n_slices,
                                                                                 int xcd_map, int nc,
-                                                                                int64_t rec_bytes,
+                                                                                int64_t rec_bytes, int nt_hint,
                                                                                 __bf16* __restrict__ states,
                                                                                 __bf16* __restrict__ ubuf) {
   constexpr bool kSave = kMode != kScanOut, kOut = kMode != kScanStates;
@@ -1025,34 +1035,59 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::threads(kMode)), 1) void chunk_
       }
     };
     // The compute waves leave each chunk's output in a double-buffered LDS tile [64][kOP]; the loaders store the
-    // previous chunk's tile during the next step as whole SL-column rows with 16-byte stores.
+    // previous chunk's tile during the next step as whole SL-column rows with 16-byte stores.  They read the tile
+    // into registers before issuing the next record copy: the compiler orders an LDS read that follows a
+    // global_load_lds behind the whole copy (s_waitcnt vmcnt(0)), which would hold the stores back until the copy
+    // had landed.
     const OutT* otile = reinterpret_cast<const OutT*>(smem + 2 * SB);
     OutT* op = static_cast<OutT*>(const_cast<void*>(a.out.ptr)) + bidx * a.out.stride_b + h * a.out.stride_h +
                bos * a.out.stride_t;
-    auto store_tile = [&](int chunk) {
-      constexpr int kPer = 16 / int(sizeof(OutT)), kRowPieces = SL / kPer;
+    constexpr int kPer = 16 / int(sizeof(OutT)), kRowPieces = SL / kPer;
+    constexpr int kTilePieces = (kRowPieces + kScanLoaders - 1) / kScanLoaders;  // 16-byte pieces per lane
+    uint4 tv[kTilePieces];
+    auto read_tile = [&](int chunk) {
       const OutT* tl = otile + (chunk & 1) * 64 * kOP;
 #pragma unroll
-      for (int pc = lw * 64 + lane; pc < 64 * kRowPieces; pc += 64 * kScanLoaders) {
-        const int row = pc / kRowPieces, col = (pc % kRowPieces) * kPer;
-        const uint4 v = *reinterpret_cast<const uint4*>(tl + row * kOP + col);
-        const int tk = chunk * kChunk + row;
-        if (tk < len) *reinterpret_cast<uint4*>(op + int64_t(tk) * a.out.stride_t + v0 + col) = v;
+      for (int i = 0; i < kTilePieces; ++i) {
+        const int pc = 64 * (lw + kScanLoaders * i) + lane;
+        if (pc < 64 * kRowPieces) tv[i] = *reinterpret_cast<const uint4*>(tl + (pc / kRowPieces) * kOP + (pc % kRowPieces) * kPer);
       }
+    };
+    auto write_tile_as = [&](int chunk, auto nt) {  // nt: std::true_type for the hinted stores
+#pragma unroll
+      for (int i = 0; i < kTilePieces; ++i) {
+        const int pc = 64 * (lw + kScanLoaders * i) + lane;
+        const int tk = chunk * kChunk + pc / kRowPieces;
+        const int64_t e = int64_t(tk) * a.out.stride_t + v0 + (pc % kRowPieces) * kPer;
+        if (pc < 64 * kRowPieces && tk < len) {
+          if constexpr (decltype(nt)::value) store_nt16(op, uint32_t(e * int64_t(sizeof(OutT))), tv[i]);
+          else *reinterpret_cast<uint4*>(op + e) = tv[i];
+        }
+      }
+    };
+    auto write_tile = [&](int chunk) {
+      if (nt_hint) write_tile_as(chunk, std::true_type{});
+      else write_tile_as(chunk, std::false_type{});
     };
     if (nchunks > 0) copy_record(0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     lds_barrier();
     for (int s = 0; s < nchunks; ++s) {
+      if constexpr (kOut) {
+        if (s > 0) read_tile(s - 1);
+      }
       if (s + 1 < nchunks) copy_record(s + 1, (s + 1) & 1);  // buffer (s + 1) & 1 held chunk s - 1: done
       if constexpr (kOut) {
-        if (s > 0) store_tile(s - 1);
+        if (s > 0) write_tile(s - 1);
       }
       __builtin_amdgcn_s_waitcnt(0);
       lds_barrier();
     }
     if constexpr (kOut) {
-      if (nchunks > 0) store_tile(nchunks - 1);
+      if (nchunks > 0) {
+        read_tile(nchunks - 1);
+        write_tile(nchunks - 1);
+      }
     }
     return;
   }
@@ -1066,18 +1101,27 @@ __global__ __launch_bounds__((ScanShape<SL, NT>::threads(kMode)), 1) void chunk_
     if constexpr (kSave) {
       const int sw = wave - kScanCompute - kScanLoaders;
       const __bf16* stile = reinterpret_cast<const __bf16*>(smem + kSaveOff);
-      auto store_save = [&](int chunk) {
+      auto store_save_as = [&](int chunk, auto nt) {  // nt: std::true_type for the hinted stores
         constexpr int kRowPieces = SL / 8, kStorers = ScanShape<SL, NT>::kStorers;
         const __bf16* sl = stile + (chunk & 1) * (K + kChunk) * kSP;
-        const size_t s0 = (size_t(n * H + h) * nc + chunk) * K * a.value_dim;
-        const size_t u0 = (size_t(n * H + h) * nc + chunk) * kChunk * a.value_dim;
+        __bf16* sc = states + (size_t(n * H + h) * nc + chunk) * K * a.value_dim;  // this chunk's state [K][V]
+        __bf16* uc = ubuf + (size_t(n * H + h) * nc + chunk) * kChunk * a.value_dim;  // and its u [64][V]
+        auto rows = [&](__bf16* base, int r0, int nrows) {  // tile rows r0 .. r0 + nrows - 1 to base's rows
 #pragma unroll
-        for (int pc = sw * 64 + lane; pc < (K + kChunk) * kRowPieces; pc += 64 * kStorers) {
-          const int row = pc / kRowPieces, col = (pc % kRowPieces) * 8;
-          const uint4 v = *reinterpret_cast<const uint4*>(sl + row * kSP + col);
-          __bf16* dst = row < K ? states + s0 + size_t(row) * a.value_dim : ubuf + u0 + size_t(row - K) * a.value_dim;
-          *reinterpret_cast<uint4*>(dst + v0 + col) = v;
-        }
+          for (int pc = sw * 64 + lane; pc < nrows * kRowPieces; pc += 64 * kStorers) {
+            const int row = pc / kRowPieces, col = (pc % kRowPieces) * 8;
+            const uint4 v = *reinterpret_cast<const uint4*>(sl + (r0 + row) * kSP + col);
+            const int e = row * a.value_dim + v0 + col;
+            if constexpr (decltype(nt)::value) store_nt16(base, uint32_t(2 * e), v);
+            else *reinterpret_cast<uint4*>(base + e) = v;
+          }
+        };
+        rows(sc, 0, K);
+        rows(uc, K, kChunk);
+      };
+      auto store_save = [&](int chunk) {
+        if (nt_hint) store_save_as(chunk, std::true_type{});
+        else store_save_as(chunk, std::false_type{});
       };
       lds_barrier();
       for (int s = 0; s < nchunks; ++s) {
@@ -1271,17 +1315,41 @@ int64_t slots_per_head(const gdr_args& a) {
   return int64_t(a.batch) * ((a.seq_len + kChunk - 1) / kChunk);
 }
 
-template <int VARIANT, int K, int kPro, typename T = __bf16>
+// Whether the call's single-use input rows (prep) and its outputs, states and u (scan) carry the non-temporal hint.
+// It pays when the records are about one to four times the 256 MB memory-side cache: the hint keeps inputs and
+// outputs from displacing the records the scan is about to read.  KDA at T = 4096, H = 16 (with the scan's output
+// tile read ahead of the record copy), by batch: B = 4 (297 MB of records) 234 -> 225 us per call, B = 6
+// 392 -> 380, B = 8 411 -> 402, B = 12 673 -> 664; the c4 variants (B = 2, T = 8192) 9-29 us faster per call; the
+// training forward at B = 4 270 -> 248 us.  Smaller calls, whose inputs stay cached from one call to the next, and
+// larger ones ran slower with the hint on every access (B = 1 96 -> 103 us, B = 2 133 -> 135, B = 16 808 -> 812,
+// the 1.5 GB packed call 3 % slower), so they go without.  The scan's hinted stores take 32-bit byte offsets from
+// each sequence's first output row, so every output row must lie within 4 GiB of it.
+template <int K>
+bool use_nt_hint(const gdr_args& a) {
+  constexpr int64_t kMin = int64_t(256) << 20, kMax = int64_t(1) << 30;
+  const int64_t records = slots_per_head(a) * a.heads * Rec<K>::bytes(a.value_dim);
+  if (records < kMin || records > kMax) return false;
+  return (int64_t(a.seq_len) * a.out.stride_t + a.value_dim) * 4 < (int64_t(1) << 32);
+}
+
+template <int VARIANT, int K, int kPro, typename T = __bf16, bool kNT = false>
 hipError_t launch_prep(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
   const int nc = (a.seq_len + kChunk - 1) / kChunk;
   const int64_t n_prep = slots_per_head(a) * a.heads;
   constexpr int prep_lds = PrepLds<K>::BYTES;
-  hipError_t e = configure_lds<&chunk_prep_kernel<VARIANT, K, kPro, T>>(prep_lds);
+  hipError_t e = configure_lds<&chunk_prep_kernel<VARIANT, K, kPro, T, kNT>>(prep_lds);
   if (e != hipSuccess) return e;
   if (n_prep > 0)
-    hipLaunchKernelGGL((chunk_prep_kernel<VARIANT, K, kPro, T>), dim3(unsigned(n_prep)), dim3(256), prep_lds, stream,
-                       a, nc, Rec<K>::bytes(a.value_dim), pro);
+    hipLaunchKernelGGL((chunk_prep_kernel<VARIANT, K, kPro, T, kNT>), dim3(unsigned(n_prep)), dim3(256), prep_lds,
+                       stream, a, nc, Rec<K>::bytes(a.value_dim), pro);
   return hipGetLastError();
+}
+
+// The plain op's prep on bf16 inputs, with the hinted input loads when the call asks for them.
+template <int VARIANT, int K>
+hipError_t launch_prep_plain(const gdr_args& a, hipStream_t stream) {
+  return use_nt_hint<K>(a) ? launch_prep<VARIANT, K, 0, __bf16, true>(a, gdr_prologue{}, stream)
+                           : launch_prep<VARIANT, K, 0>(a, gdr_prologue{}, stream);
 }
 
 }  // namespace
@@ -1326,7 +1394,7 @@ hipError_t launch_scan_sl(const gdr_args& a, int nc, __bf16* states, __bf16* ubu
   const int n_slices = a.value_dim / SL;
   const int xcd_map = (bh % 8 == 0) ? 1 : 0;
   hipLaunchKernelGGL(kernel, dim3(bh * n_slices), dim3(Sh::threads(kMode)), scan_lds, stream, a, n_slices, xcd_map, nc,
-                     Rec<K>::bytes(a.value_dim), states, ubuf);
+                     Rec<K>::bytes(a.value_dim), int(use_nt_hint<K>(a)), states, ubuf);
   return hipGetLastError();
 }
 
@@ -1357,7 +1425,7 @@ hipError_t launch_split_typed(const gdr_args& a, const gdr_prologue& pro, hipStr
   const bool conv = pro.flags & GDR_PRO_CONV;
   const bool any_width = conv && pro.conv_size != 4;  // widths other than 4: one kernel per mode for all of them
   if (!pro.flags) {
-    e = launch_prep<VARIANT, K, 0>(a, pro, stream);
+    e = launch_prep_plain<VARIANT, K>(a, stream);
   } else if constexpr (VARIANT == GDR_KDA || VARIANT == GDR_GLA) {
     if (pro.flags & GDR_PRO_GATE_LOWRANK)
       e = !conv ? launch_prep<VARIANT, K, 2>(a, pro, stream)
@@ -1393,7 +1461,7 @@ hipError_t launch_states_typed(const gdr_args& fwd, const BwdLayout& L, unsigned
   gdr_args a = fwd;
   a.workspace = ws + L.rec;
   a.ht = nullptr;
-  hipError_t e = launch_prep<VARIANT, K, 0>(a, gdr_prologue{}, stream);
+  hipError_t e = launch_prep_plain<VARIANT, K>(a, stream);
   if (e != hipSuccess) return e;
   return launch_scan<VARIANT, K, __bf16, kScanStates>(a, reinterpret_cast<__bf16*>(ws + L.states),
                                               reinterpret_cast<__bf16*>(ws + L.ubuf), stream);
@@ -1405,7 +1473,7 @@ template <int VARIANT, int K>
 hipError_t launch_train_typed(const gdr_args& fwd, const BwdLayout& L, unsigned char* ws, hipStream_t stream) {
   gdr_args a = fwd;
   a.workspace = ws + L.rec;
-  hipError_t e = launch_prep<VARIANT, K, 0>(a, gdr_prologue{}, stream);
+  hipError_t e = launch_prep_plain<VARIANT, K>(a, stream);
   if (e != hipSuccess) return e;
   __bf16* states = reinterpret_cast<__bf16*>(ws + L.states);
   __bf16* ubuf = reinterpret_cast<__bf16*>(ws + L.ubuf);
