@@ -290,7 +290,7 @@ __device__ __forceinline__ void lowrank_gate_rows(const gdr_prologue& pro, int h
 
 // ======================================= prep: one workgroup per (chunk, head) =======================================
 // 16 bytes of an input row that only this workgroup reads: with the non-temporal hint when kNT.
-template <bool kNT, typename R>
+template <int kNT, typename R>
 __device__ __forceinline__ R input16(const void* p) {
   if constexpr (kNT) return load_nt16<R>(p);
   else return *static_cast<const R*>(p);
@@ -303,7 +303,7 @@ __device__ __forceinline__ R input16(const void* p) {
 // f16 build, whose diagonal strip tile carries extra bf16 operands, and the any-width convolution, whose widest
 // path holds 11 input rows and 8 weight rows per thread, are held to two so that they do not spill.  kNT (plain
 // op only): the q, k, gate and V rows are loaded with the non-temporal hint (`use_nt_hint` below decides).
-template <int VARIANT, int K, int kPro = 0, typename T = __bf16, bool kNT = false>
+template <int VARIANT, int K, int kPro = 0, int kNT = 0, typename T = __bf16>
 __global__ __launch_bounds__(256, (__is_same(T, _Float16) || (kPro & 16)) ? 2 : 3) void chunk_prep_kernel(const gdr_args a, int nc,
                                                                                          int64_t rec_bytes,
                                                                                          const gdr_prologue pro) {
@@ -1332,15 +1332,15 @@ bool use_nt_hint(const gdr_args& a) {
   return (int64_t(a.seq_len) * a.out.stride_t + a.value_dim) * 4 < (int64_t(1) << 32);
 }
 
-template <int VARIANT, int K, int kPro, typename T = __bf16, bool kNT = false>
+template <int VARIANT, int K, int kPro, typename T = __bf16, int kNT = 0>
 hipError_t launch_prep(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
   const int nc = (a.seq_len + kChunk - 1) / kChunk;
   const int64_t n_prep = slots_per_head(a) * a.heads;
   constexpr int prep_lds = PrepLds<K>::BYTES;
-  hipError_t e = configure_lds<&chunk_prep_kernel<VARIANT, K, kPro, T, kNT>>(prep_lds);
+  hipError_t e = configure_lds<&chunk_prep_kernel<VARIANT, K, kPro, kNT, T>>(prep_lds);
   if (e != hipSuccess) return e;
   if (n_prep > 0)
-    hipLaunchKernelGGL((chunk_prep_kernel<VARIANT, K, kPro, T, kNT>), dim3(unsigned(n_prep)), dim3(256), prep_lds,
+    hipLaunchKernelGGL((chunk_prep_kernel<VARIANT, K, kPro, kNT, T>), dim3(unsigned(n_prep)), dim3(256), prep_lds,
                        stream, a, nc, Rec<K>::bytes(a.value_dim), pro);
   return hipGetLastError();
 }
@@ -1348,7 +1348,7 @@ hipError_t launch_prep(const gdr_args& a, const gdr_prologue& pro, hipStream_t s
 // The plain op's prep on bf16 inputs, with the hinted input loads when the call asks for them.
 template <int VARIANT, int K>
 hipError_t launch_prep_plain(const gdr_args& a, hipStream_t stream) {
-  return use_nt_hint<K>(a) ? launch_prep<VARIANT, K, 0, __bf16, true>(a, gdr_prologue{}, stream)
+  return use_nt_hint<K>(a) ? launch_prep<VARIANT, K, 0, __bf16, 1>(a, gdr_prologue{}, stream)
                            : launch_prep<VARIANT, K, 0>(a, gdr_prologue{}, stream);
 }
 
