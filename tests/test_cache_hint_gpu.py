@@ -8,13 +8,15 @@ computed on its own, so a hinted call must equal the same work done as smaller, 
 * the forward at the c2 shape (B = 4, T = 4096, H = 16, 291 MB of records, hinted) against its two halves along
   the sequence (145 MB each, unhinted) chained through the fp32 state, which keeps the scan's slice width;
 * the forward at the c2 and c4 shapes against each batch element run alone (unhinted, narrower scan slices);
-* the training forward and backward at the c2 shape against each batch element's own training step.
+* the training forward and backward at the c2 shape against each batch element's own training step;
+* the fused-prologue call at the c2 shape (with and without the in-kernel convolutions) against each batch
+  element's own call.
 """
 
 import pytest
 import torch
 
-from _helpers import CHUNK_FNS, oracle, workloads
+from _helpers import CHUNK_FNS, gdr, oracle, workloads
 
 pytestmark = pytest.mark.gpu
 
@@ -89,3 +91,38 @@ def test_hinted_training_step_equals_each_batch_element_alone():
         torch.cuda.synchronize()
         for name, x, y in zip(names, full, part):
             assert torch.equal(x[b:b + 1], y), (name, b)
+
+
+@pytest.mark.parametrize("conv", [False, True])
+def test_hinted_fused_call_equals_each_batch_element_alone(conv):
+    """The fused-prologue call (low-rank gate, optionally the short convolutions) at the c2 shape, whose scan stores
+    its output with the hint, against each batch element's own call."""
+    B, T, H, K, V, R = 4, 4096, 16, 128, 128, 128
+    print(f"fused kda B{B} T{T} H{H} (convolutions: {conv}): one call against each element alone", flush=True)
+    gen = torch.Generator().manual_seed(25)
+    q = (torch.randn(B, H, T, K, generator=gen) * 3.0).bfloat16().cuda()
+    k = (torch.randn(B, H, T, K, generator=gen) * 3.0).bfloat16().cuda()
+    v = torch.randn(B, H, T, V, generator=gen).bfloat16().cuda()
+    z = torch.randn(B, T, R, generator=gen).bfloat16().cuda()
+    w = (torch.randn(H * K, R, generator=gen) / R ** 0.5).bfloat16().cuda()
+    bias = torch.full((H * K,), -4.0).cuda()
+    a_log = torch.log(torch.empty(H).uniform_(1, 16, generator=gen)).cuda()
+    logits = torch.randn(B, H, T, generator=gen).cuda()
+    h0 = (torch.randn(B, H, K, V, generator=gen) * 0.02).cuda()
+    kw = {}
+    if conv:  # q, k, v are then the convolutions' inputs, read as [B, T, C] rows
+        C = H * K
+        flat = lambda x: x.transpose(1, 2).contiguous().view(B, T, C)
+        q, k, v = (flat(x).view(B, T, H, -1).transpose(1, 2) for x in (q, k, v))
+        kw["conv_weights"] = [((torch.rand(C, 1, 4, generator=gen) * 2 - 1) * 0.5).bfloat16().cuda() for _ in range(3)]
+
+    def call(b):
+        with torch.no_grad():
+            return gdr.chunk_kimi_delta_attention_fused(q[b], k[b], v[b], z[b], w, bias, a_log, logits[b],
+                                                        initial_state=h0[b], output_final_state=True, **kw)
+
+    out, state = call(slice(None))
+    for b in range(B):
+        ob, sb = call(slice(b, b + 1))
+        torch.cuda.synchronize()
+        assert torch.equal(out[b:b + 1], ob) and torch.equal(state[b:b + 1], sb), b
