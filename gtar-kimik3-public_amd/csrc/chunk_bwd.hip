@@ -384,6 +384,46 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
   const __bf16* ug = ubuf + cidx * kChunk * V;  // u [64][V]
   const __bf16* dop = static_cast<const __bf16*>(g.d_out.ptr) + n * g.d_out.stride_b + h * g.d_out.stride_h;
 
+  // dO and u columns of the first kPre value passes (token rows) and du^T rows of those columns, copied into their
+  // swizzled LDS buffers (global_load_lds_dwordx4: lane i lands at the wave's base + 16 i, i.e. row 8 (m mod 8) + i / 8
+  // of the buffer, slot i % 8, which holds chunk (i % 8) ^ (row % 8) of the row) by `nw` waves from wave w0 of them.
+  // dO rows past the sequence end read its last row; they and the u rows there are zeroed once the copies have landed,
+  // and du^T's columns there are masked where they are used.  The compiler orders every LDS read that follows a
+  // global_load_lds in the same wave behind the whole copy, so with eight waves (and a delta rule) the copies are
+  // issued by waves 4..7 after the P tiles, which then have no LDS reads until after the inverse (that waves 0..3
+  // compute meanwhile); otherwise they go out behind the row loads.
+  constexpr bool kLateCopies = NW >= 8 && kDelta;
+  auto copy_pass_buffers = [&](int w0, int nw) {
+    const int npre = min(V / 64, L::kPre);
+#pragma unroll
+    for (int k = 0; k < 3 * L::kPre * 8 / (kLateCopies ? NW / 2 : NW); ++k) {
+      const int m = w0 + nw * k, ps = m / 24, tn = (m >> 3) % 3, row = 8 * (m & 7) + (lane >> 3);
+      const int chunk8 = 8 * ((lane & 7) ^ (row & 7)), col = 64 * ps + chunk8;
+      const __bf16* src = tn == 0   ? dop + (t0 + min(row, nvalid - 1)) * int64_t(g.d_out.stride_t) + col
+                          : tn == 1 ? ug + size_t(row) * V + col
+                                    : dubt + (cidx * V + 64 * ps + row) * kChunk + chunk8;
+      if (ps < npre)
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(smem + L::DOU + m * 1024),
+                                         16, 0, 0);
+    }
+  };
+  // The workgroup barriers of the P tiles and the inverse, which the late copies are in flight across: the
+  // compiler's LDS release fence would wait for them (it counts the copies as LDS writes, on vmcnt), so this one
+  // waits for the wave's own LDS operations only.  The copies are waited for before the passes read them.
+  auto copy_barrier = [&]() {
+    if constexpr (kLateCopies) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else lds_barrier();
+  };
+  auto zero_past_end = [&]() {  // the prefetched dO and u rows past the sequence end become zeros
+    if (nvalid < kChunk) {
+      for (int idx = tid; idx < L::kPre * 2 * 64 * 8; idx += 64 * NW) {
+        const int ps = idx >> 10, tn = (idx >> 9) & 1, row = (idx >> 3) & 63;
+        if (row >= nvalid)
+          *reinterpret_cast<uint4*>(smem + L::DOU + (3 * ps + tn) * L::PB + 16 * (idx & 511)) = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+
   // ---- 1. row-owned (block p = w mod 4; lane: row 16 p + l16, channels 32 kk + 8 g4 + j for this wave's KH channel
   // groups kk0 .. kk0 + KH - 1; with eight waves, waves p and p + 4 take the two halves of the channels): q, k rows
   // into LDS; the log2-gate cumsum within the block (b); P's operands k e^{b} (A), k e^{b_15 - b} (B, via LDS) and
@@ -422,25 +462,7 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
         for (int j = 0; j < 8; ++j) bl[x][j] = gs;
       }
     }
-    // dO and u columns of the first kPre value passes (token rows) and du^T rows of those columns, copied into
-    // their swizzled LDS buffers behind the row loads (global_load_lds_dwordx4: lane i lands at the wave's base +
-    // 16 i, i.e. row 8 (m mod 8) + i / 8 of the buffer, slot i % 8, which holds chunk (i % 8) ^ (row % 8) of the
-    // row).  dO rows past the sequence end read its last row; they and the u rows there are zeroed once the copies
-    // have landed (step 1b), and du^T's columns there are masked where they are used.
-    {
-      const int npre = min(V / 64, L::kPre);
-#pragma unroll
-      for (int k = 0; k < 3 * L::kPre * 8 / NW; ++k) {
-        const int m = w + NW * k, ps = m / 24, tn = (m >> 3) % 3, row = 8 * (m & 7) + (lane >> 3);
-        const int chunk8 = 8 * ((lane & 7) ^ (row & 7)), col = 64 * ps + chunk8;
-        const __bf16* src = tn == 0   ? dop + (t0 + min(row, nvalid - 1)) * int64_t(g.d_out.stride_t) + col
-                            : tn == 1 ? ug + size_t(row) * V + col
-                                      : dubt + (cidx * V + 64 * ps + row) * kChunk + chunk8;
-        if (ps < npre)
-          __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(smem + L::DOU + m * 1024),
-                                           16, 0, 0);
-      }
-    }
+    if constexpr (!kLateCopies) copy_pass_buffers(w, NW);
     if (kDelta && kk0 == 0 && g4 == 0) BETA[trow] = valid ? betap[tc * a.beta.stride_t] : 0.f;
     const float kf = valid ? kLog2e : 0.f;
 #pragma unroll
@@ -475,18 +497,12 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
     }
   }
 
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's pass-buffer copies have landed
+  if constexpr (!kLateCopies) __builtin_amdgcn_s_waitcnt(0);  // this wave's pass-buffer copies have landed
   lds_barrier();
 
   // ---- 1b. column-owned (every wave, channel d): the in-chunk log2-gate cumsum B at rows 16 j + 4 g4 + r, the
   // block-local cumsum plus the totals of the blocks before ----
-  if (nvalid < kChunk) {  // the prefetched dO and u rows past the sequence end become zeros
-    for (int idx = tid; idx < L::kPre * 2 * 64 * 8; idx += 64 * NW) {
-      const int ps = idx >> 10, tn = (idx >> 9) & 1, row = (idx >> 3) & 63;
-      if (row >= nvalid)
-        *reinterpret_cast<uint4*>(smem + L::DOU + (3 * ps + tn) * L::PB + 16 * (idx & 511)) = make_uint4(0u, 0u, 0u, 0u);
-    }
-  }
+  if constexpr (!kLateCopies) zero_past_end();
   float bc[4][4];
   {
     float pre = 0.f;
@@ -547,6 +563,9 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
     }
   }
   lds_barrier();  // the q and k rows are read: R1 takes P, R2 takes A
+  if constexpr (kLateCopies) {
+    if (w >= NW / 2) copy_pass_buffers(w - NW / 2, NW / 2);
+  }
 
   // v rows for rowsum(X2 (x) V), loaded one value pass ahead of their use (the first pass's before the inverse)
   auto load_vv = [&](int v0, bf16x4 (&dst)[NRT]) {
@@ -607,7 +626,7 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
         }
       }
     }
-    lds_barrier();
+    copy_barrier();
 
     // ---- 3. A = (I + diag(beta) P)^{-1} (waves 0..3): diagonal blocks by forward substitution, then block rows
     // 1..3 on fp32 MFMA with wave p owning tile column p ----
@@ -631,7 +650,7 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
         if (col >= 16 * (p + 1) || col < 16 * p) AL[(16 * p + x) * MP + col] = 0.f;
       }
     }
-    lds_barrier();
+    copy_barrier();
     // Y = diag(beta) P[block i, :16 i] A[:16 i, block p] (wave-private scratch), A_ip = -A_ii Y (zero for p >= i).
     // Wave p reads only column block p of A (its own writes, and the zeros and diagonal blocks in place before the
     // barrier above), A_ii and its own scratch, so the block rows need no barrier between them: a wave's LDS
@@ -657,7 +676,7 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
         }
       }
     }
-    lds_barrier();
+    copy_barrier();
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -673,7 +692,12 @@ __global__ __launch_bounds__(64 * (K / 16)) void chunk_dlocal_kernel(const gdr_a
 #pragma unroll
       for (int e = 0; e < 8; ++e) aB[kb][e] = bf(32 * kb + 8 * g4 + e == 16 * tb + l16 ? 1.f : 0.f);
   }
+  if constexpr (kLateCopies) __builtin_amdgcn_s_waitcnt(0);  // this wave's pass-buffer copies have landed
   lds_barrier();  // P and A are read: R1 .. R3 take the pass buffers
+  if constexpr (kLateCopies) {
+    zero_past_end();
+    if (nvalid < kChunk) lds_barrier();
+  }
 
   // ---- 4. passes over 64 value columns: X2 (dv, dbeta), then X1, dQd, dKt (channel tile w, all rows) and dSc,
   // dL (columns of block tb, this wave's row tiles), and bnd = rowsum(S (x) dS') of channel d ----
