@@ -960,6 +960,8 @@ struct ScanShape {
 // at 16 heads, a simulation of the dispatch gives a makespan of 171 steps against 199 (166 with no tail at all).
 // One workgroup ranks the sequences by length (descending, ties by index): seq_order[r] is the sequence of rank r.
 constexpr int kSeqOrderMax = 512;  // packed calls with more sequences keep the index order
+// Whether a packed call's workspace holds the order (its size does not depend on the device).
+inline bool seq_order_room(const gdr_args& a) { return a.cu_seqlens && a.n_seqs >= 2 && a.n_seqs <= kSeqOrderMax; }
 __global__ __launch_bounds__(kSeqOrderMax) void seq_order_kernel(const int32_t* __restrict__ cu, int n_seqs, int T,
                                                                  int32_t* __restrict__ order) {
   __shared__ int lens[kSeqOrderMax];
@@ -1438,10 +1440,14 @@ hipError_t launch_scan(const gdr_args& a, __bf16* states, __bf16* ubuf, hipStrea
   return launch_scan_sl<VARIANT, K, OutT, 16, 1, kMode, T>(a, nc, states, ubuf, seq_order, stream);
 }
 
-// The longest-first order of a packed call's sequences, written into the workspace after the records (NULL when the
-// call is not packed or has more than kSeqOrderMax sequences).
+// The longest-first order of a packed call's sequences, written into the workspace after the records.  NULL (index
+// order) when the call is not packed, has more than kSeqOrderMax sequences, or launches no more scan workgroups than
+// there are CUs (they then all start at once and the order cannot matter; the ranking launch costs about 5 us).
 int32_t* launch_seq_order(const gdr_args& a, int64_t records, hipStream_t stream) {
-  if (!a.cu_seqlens || a.n_seqs < 2 || a.n_seqs > kSeqOrderMax) return nullptr;
+  if (!seq_order_room(a)) return nullptr;
+  if (int64_t(a.n_seqs) * a.heads * (a.value_dim / scan_slice(int64_t(a.n_seqs) * a.heads, a.value_dim)) <=
+      device_cus())
+    return nullptr;
   int32_t* order = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(a.workspace) + records);
   hipLaunchKernelGGL(seq_order_kernel, dim3(1), dim3(kSeqOrderMax), 0, stream, a.cu_seqlens, a.n_seqs, a.seq_len,
                      order);
@@ -1532,8 +1538,7 @@ hipError_t launch_states_v(const gdr_args& a, const BwdLayout& L, unsigned char*
 
 int64_t chunk_workspace_bytes(const gdr_args& a) {
   const int64_t rec = a.key_dim == 64 ? Rec<64>::bytes(a.value_dim) : Rec<128>::bytes(a.value_dim);
-  const bool order = a.cu_seqlens && a.n_seqs >= 2 && a.n_seqs <= kSeqOrderMax;  // launch_seq_order's array
-  return slots_per_head(a) * a.heads * rec + (order ? (int64_t(a.n_seqs) * 4 + 255) / 256 * 256 : 0);
+  return slots_per_head(a) * a.heads * rec + (seq_order_room(a) ? (int64_t(a.n_seqs) * 4 + 255) / 256 * 256 : 0);
 }
 
 hipError_t launch_chunk_states(const gdr_args& a, const BwdLayout& L, unsigned char* ws, hipStream_t stream) {
