@@ -139,8 +139,9 @@ int gdr_chunk_fwd_fused(const gdr_args* args, const gdr_prologue* pro, hipStream
  * that the chunk-parallel preparation kernel writes and the state-scan kernel reads: the reference keeps the
  * same kind of intermediates (gate cumsum, P, A, W, U, States) in tensors it allocates per call
  * (src/ops/kimi_delta_attention.py:540-553).  For B=4, T=4096, H=16, K=V=128 it is 291.5 MB (71,168 bytes per
- * chunk and head).  The size does not depend on dtypes; it is 0 for key dims the chunk kernels do not take (the
- * sequential path needs no workspace, and ignores one it is given, as f32 calls do). */
+ * chunk and head).  A packed call with 2 to 512 sequences adds their longest-first order for the state scan
+ * (n_seqs int32, rounded up to 256 bytes).  The size does not depend on dtypes; it is 0 for key dims the chunk
+ * kernels do not take (the sequential path needs no workspace, and ignores one it is given, as f32 calls do). */
 int64_t gdr_chunk_workspace_bytes(const gdr_args* args);
 
 /* Size of the device scratch behind gdr_chunk_fwd_noalloc (128 MiB per GPU). */
