@@ -13,6 +13,9 @@ computed on its own, so a hinted call must equal the same work done as smaller, 
   element's own call.
 """
 
+import ctypes
+import importlib
+
 import pytest
 import torch
 
@@ -55,13 +58,24 @@ def test_hinted_forward_equals_its_halves_along_the_sequence():
     assert torch.equal(out, torch.cat([o1, o2], dim=2)) and torch.equal(state, s2)
 
 
-@pytest.mark.parametrize("variant,batch,seq_len", [("kda", 4, 4096)] +
-                         [(v, 2, 8192) for v in oracle.VARIANTS])
-def test_hinted_forward_equals_each_batch_element_alone(variant, batch, seq_len):
+def _record_bytes(K, V):
+    """Bytes of one (chunk, head) record, as gdr_chunk_workspace_bytes reports them for a one-chunk, one-head call."""
+    lib = importlib.import_module("gtar-kimik3-public_amd._lib")
+    x = lambda d: torch.empty(1, 1, 64, d, dtype=torch.bfloat16)
+    args = lib.make_args(lib.KDA, x(K), x(K), x(V), torch.empty(1, 1, 64, K), torch.empty(1, 1, 64), x(V), 1.0,
+                         None, None)
+    return lib.load_library().gdr_chunk_workspace_bytes(ctypes.byref(args))
+
+
+@pytest.mark.parametrize("variant,batch,seq_len,K,V", [("kda", 4, 4096, 128, 128), ("kda", 4, 4096, 128, 256),
+                                                       ("kda", 16, 4096, 64, 64)] +
+                         [(v, 2, 8192, 128, 128) for v in oracle.VARIANTS])
+def test_hinted_forward_equals_each_batch_element_alone(variant, batch, seq_len, K, V):
     H = 16
-    assert _records(batch, seq_len, H) >= 256 << 20 > _records(1, seq_len, H)
-    print(f"{variant} B{batch} T{seq_len} H{H}: one call against each element alone", flush=True)
-    inp = workloads.make_inputs(variant, batch, seq_len, H, 128, 128, seed=22, state_std=0.02, device="cuda")
+    rec = _record_bytes(K, V)
+    assert batch * (seq_len // 64) * H * rec >= 256 << 20 > (seq_len // 64) * H * rec
+    print(f"{variant} B{batch} T{seq_len} H{H} K{K} V{V}: one call against each element alone", flush=True)
+    inp = workloads.make_inputs(variant, batch, seq_len, H, K, V, seed=22, state_std=0.02, device="cuda")
     out, state = _fwd(variant, inp)
     for b in range(batch):
         ob, sb = _fwd(variant, _part(inp, b=slice(b, b + 1)))
