@@ -1443,20 +1443,24 @@ hipError_t launch_scan(const gdr_args& a, __bf16* states, __bf16* ubuf, hipStrea
 // The longest-first order of a packed call's sequences, written into the workspace after the records.  NULL (index
 // order) when the call is not packed, has more than kSeqOrderMax sequences, or launches no more scan workgroups than
 // there are CUs (they then all start at once and the order cannot matter; the ranking launch costs about 5 us).
-int32_t* launch_seq_order(const gdr_args& a, int64_t records, hipStream_t stream) {
-  if (!seq_order_room(a)) return nullptr;
+hipError_t launch_seq_order(const gdr_args& a, int64_t records, const int32_t** order, hipStream_t stream) {
+  *order = nullptr;
+  if (!seq_order_room(a)) return hipSuccess;
   if (int64_t(a.n_seqs) * a.heads * (a.value_dim / scan_slice(int64_t(a.n_seqs) * a.heads, a.value_dim)) <=
       device_cus())
-    return nullptr;
-  int32_t* order = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(a.workspace) + records);
-  hipLaunchKernelGGL(seq_order_kernel, dim3(1), dim3(kSeqOrderMax), 0, stream, a.cu_seqlens, a.n_seqs, a.seq_len,
-                     order);
-  return order;
+    return hipSuccess;
+  int32_t* o = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(a.workspace) + records);
+  hipLaunchKernelGGL(seq_order_kernel, dim3(1), dim3(kSeqOrderMax), 0, stream, a.cu_seqlens, a.n_seqs, a.seq_len, o);
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) *order = o;  // the scan reads the order only when it was written
+  return e;
 }
 
 template <int VARIANT, int K, typename OutT>
 hipError_t launch_split_typed(const gdr_args& a, const gdr_prologue& pro, hipStream_t stream) {
-  const int32_t* order = launch_seq_order(a, slots_per_head(a) * a.heads * Rec<K>::bytes(a.value_dim), stream);
+  const int32_t* order;
+  const hipError_t oe = launch_seq_order(a, slots_per_head(a) * a.heads * Rec<K>::bytes(a.value_dim), &order, stream);
+  if (oe != hipSuccess) return oe;
   if (a.q.dtype == GDR_F16) {  // f16 q, k, v: f16 MFMA operands and records (plain op only)
     hipError_t e = launch_prep<VARIANT, K, 0, _Float16>(a, pro, stream);
     if (e != hipSuccess) return e;
