@@ -191,6 +191,33 @@ def test_short_convolution_empty_sequences_keep_their_state(dtype):
             assert torch.equal(st[n].cpu(), state[n])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("width", [2, 3, 4, 5, 6, 7, 8])
+def test_short_convolution_tile_paths_agree(dtype, width):
+    """Sequence lengths around the kernel's 8-token tiles.  A tile inside one sequence takes the register path, a
+    tile at a sequence's start or end the token-by-token path; packed, a sequence's tokens sit at other tile offsets
+    than when it runs alone, so the packed call equal to each sequence run alone (with its own state) bit for bit
+    holds the two paths to the same arithmetic.  Both meet the oracle, and the new states are exact copies."""
+    lens = [7, 8, 9, 1, 15, 16, 17, 3, 40, 2]
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
+    T, C = int(cu[-1]), 48
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn(1, T, C, generator=gen).to(dtype)
+    w = (torch.randn(C, 1, width, generator=gen) * 0.5).to(dtype)
+    state = torch.randn(len(lens), C, width - 1, generator=gen).to(dtype)
+    ref, ref_state = oracle.short_convolution(x, w, state, cu)
+    st = state.cuda()
+    with torch.no_grad():
+        out = gdr.short_convolution(x.cuda(), w.cuda(), st, cu_seqlens=cu.cuda()).cpu()
+        for n, (s, e) in enumerate(zip(cu[:-1].tolist(), cu[1:].tolist())):
+            st_n = state[n:n + 1].cuda()
+            alone = gdr.short_convolution(x[:, s:e].cuda(), w.cuda(), st_n).cpu()
+            assert torch.equal(alone, out[:, s:e]), (n, s, e)
+            assert torch.equal(st_n[0].cpu(), st[n].cpu()), n
+    assert ((out.double() - ref).abs().max() / ref.abs().max()).item() <= 1e-2
+    assert torch.equal(st.cpu(), ref_state.to(dtype))
+
+
 def test_short_convolution_zero_tokens_keeps_the_state():
     """T == 0 launches nothing; the state passed in comes back unchanged."""
     gen = torch.Generator().manual_seed(7)
