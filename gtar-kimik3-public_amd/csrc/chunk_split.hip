@@ -130,7 +130,7 @@ __device__ __forceinline__ void conv_silu8x4(const __bf16* x0, int64_t x_st, int
     }
     bf16x8 o;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = bf(acc[e] / (1.f + __builtin_amdgcn_exp2f(-acc[e] * kLog2e)));
+    for (int e = 0; e < 8; ++e) o[e] = bf(silu_rcp(acc[e]));
     out[i] = __builtin_bit_cast(uint4, o);
   }
 }
@@ -146,7 +146,7 @@ __device__ __forceinline__ float conv_silu1(const __bf16* x0, int64_t x_st, int 
     const float xv = r >= 0 ? f32(x0[int64_t(r) * x_st]) : (st ? f32(st[(W - 1) + r]) : 0.f);
     acc += f32(ww[j]) * xv;
   }
-  return f32(bf(acc / (1.f + __builtin_amdgcn_exp2f(-acc * kLog2e))));
+  return f32(bf(silu_rcp(acc)));
 }
 
 // Calls f(IntC<W>{}) for a convolution width known at run time (2 to 8, uniform over the workgroup; validated by

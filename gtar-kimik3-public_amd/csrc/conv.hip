@@ -32,7 +32,7 @@ __device__ __forceinline__ int seq_of(const int32_t* cu, int n_seqs, int t) {
 constexpr int kConvTok = 8;  // consecutive tokens per thread: the W - 1 shared input rows are loaded once
 
 __device__ __forceinline__ float silu_or_not(float acc, bool silu) {
-  return silu ? acc / (1.f + __builtin_amdgcn_exp2f(-acc * 1.4426950408889634f)) : acc;
+  return silu ? silu_rcp(acc) : acc;
 }
 
 template <typename T, int W>

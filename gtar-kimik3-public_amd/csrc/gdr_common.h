@@ -42,6 +42,13 @@ __device__ __forceinline__ void store_any(void* p, int64_t i, int dtype, float x
 // e^x through the hardware 2^x instruction (v_exp_f32) with a log2(e) pre-scale.
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 
+// SiLU x / (1 + e^-x) of the short convolutions, with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE
+// division (about ten instructions): the standalone and the in-kernel convolutions share it, so their results agree
+// bit for bit.
+__device__ __forceinline__ float silu_rcp(float x) {
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
+
 __device__ __forceinline__ float shfl_xor(float x, int mask) { return __shfl_xor(x, mask, kWave); }
 
 // x + x[lane ^ m] in every lane (m a power of two below 64, constant after unrolling), formed on the VALU where one
