@@ -367,17 +367,24 @@ __global__ __launch_bounds__(256, (__is_same(T, _Float16) || (kPro & 16)) ? 2 : 
     const __bf16* st = static_cast<const __bf16*>(pro.conv_state_in[i]);
     return st ? st + (int64_t(n) * nch + ch0) * (cw - 1) : nullptr;
   };
-  // 8 channels x 4 rows of the convolution at the call's width
-  auto conv8x4 = [&](const __bf16* x0, int64_t x_st, int r0, const __bf16* w8, const __bf16* st8, uint4 (&o)[4]) {
+  // 8 channels x 4 rows of the convolution at the call's width.  Inlined by force: as a called function its output
+  // array went through scratch memory.
+  auto conv8x4 = [&](const __bf16* x0, int64_t x_st, int r0, const __bf16* w8, const __bf16* st8,
+                     uint4 (&o)[4]) __attribute__((always_inline)) {
     if constexpr (kAnyWidth)
-      with_conv_width(cw, [&](auto wc) { conv_silu8x4<decltype(wc)::value>(x0, x_st, r0, len - 1, w8, st8, o); });
+      with_conv_width(cw, [&](auto wc) __attribute__((always_inline)) {
+        conv_silu8x4<decltype(wc)::value>(x0, x_st, r0, len - 1, w8, st8, o);
+      });
     else
       conv_silu8x4<4>(x0, x_st, r0, len - 1, w8, st8, o);
   };
-  auto conv1 = [&](const __bf16* x0, int64_t x_st, int t, const __bf16* ww, const __bf16* st) {
+  auto conv1 = [&](const __bf16* x0, int64_t x_st, int t, const __bf16* ww, const __bf16* st)
+                   __attribute__((always_inline)) {
     float r = 0.f;
     if constexpr (kAnyWidth)
-      with_conv_width(cw, [&](auto wc) { r = conv_silu1<decltype(wc)::value>(x0, x_st, t, ww, st); });
+      with_conv_width(cw, [&](auto wc) __attribute__((always_inline)) {
+        r = conv_silu1<decltype(wc)::value>(x0, x_st, t, ww, st);
+      });
     else
       r = conv_silu1<4>(x0, x_st, t, ww, st);
     return r;
